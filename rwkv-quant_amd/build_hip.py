@@ -1,0 +1,46 @@
+"""Build librwkvq_hip.so from csrc/*.hip for gfx950 with hipcc.
+
+    python rwkv-quant_amd/build_hip.py
+
+The shared library lands in rwkv_quant/backends/hip/ (in-tree), next to
+its ctypes binding.
+"""
+import glob
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+OUT = os.path.join(HERE, "rwkv_quant", "backends", "hip", "librwkvq_hip.so")
+ARCH = os.environ.get("RWKVQ_OFFLOAD_ARCH", "gfx950")
+
+FLAGS = [
+    "-O3", "-std=c++17", "-shared", "-fPIC", f"--offload-arch={ARCH}",
+    # keep the compiler from forming packed fp32 instructions
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-I", os.path.join(ROOT, "include"), "-I", CSRC,
+]
+
+
+def build(verbose=True):
+    srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+    tmp = OUT + ".tmp"
+    cmd = ["hipcc", *FLAGS, *srcs, "-o", tmp]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "is not a recognized feature for this target"
+    err = "\n".join(l for l in r.stderr.splitlines() if noise not in l)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({r.returncode}):\n{err}")
+    if err.strip() and verbose:
+        print(err)
+    os.replace(tmp, OUT)
+    return OUT
+
+
+if __name__ == "__main__":
+    print(build())
+    sys.exit(0)

@@ -1,0 +1,158 @@
+// Bit-exact fp32 dequantization of the device layouts (the checker the
+// GEMV/GEMM kernels are compared against, and the load-time expansion of
+// LoRA tensors).  Arithmetic follows the format formulas with their fp16
+// round trips and with products and sums rounded separately (no FMA
+// contraction), exactly as the numpy reference computes them
+// (reference: rwkv_quant/formats/codec.py:183-292).
+#include "rwkvq_common.h"
+
+// products and sums must round separately, as numpy does: forbid the
+// a*b+c -> fma contraction hipcc applies by default
+#pragma clang fp contract(off)
+
+using namespace rwkvq;
+
+namespace {
+
+// code bits 4/5 of column c (0..31) of a 32-column group from the device
+// high-bit words.  `pair_of` maps the column to (pair i, half).
+__device__ __forceinline__ uint32_t high_bits_crumb(const uint32_t* hw, int i,
+                                                    int half) {
+  uint32_t H = hw[i >> 3];
+  int sh = 2 * (i & 7) + 16 * half;
+  return (H >> sh) & 3u;
+}
+
+__global__ void dq_sb6(const uint8_t* nib, const uint32_t* hb,
+                       const uint8_t* rec, int bits, int rows, int in,
+                       float* w, int ld) {
+  const int ng = in >> 5, nsb = in >> 8;
+  long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (long)rows * ng) return;
+  const int row = (int)(t / ng), g = (int)(t % ng);
+  const uint8_t* rp = rec + ((size_t)row * nsb + (g >> 3)) * 16;
+  const int kb = g & 7;
+  // 6-bit fields of the 48-bit qs stream and the 48-bit qm stream
+  uint64_t s0 = 0, s1 = 0;
+  for (int b = 0; b < 6; ++b) {
+    s0 |= (uint64_t)rp[b] << (8 * b);
+    s1 |= (uint64_t)rp[6 + b] << (8 * b);
+  }
+  const uint32_t qs = (uint32_t)(s0 >> (6 * kb)) & 63u;
+  const int qm = (int)((uint32_t)(s1 >> (6 * kb)) & 63u) - 31;
+  const float d = f16_bits_to_f32(rp[12] | (rp[13] << 8));
+  const float dm = f16_bits_to_f32(rp[14] | (rp[15] << 8));
+  const float s = fmaxf(f16_round(((float)qs * d)), 1e-8f);
+  const float m = f16_round(((float)qm * dm));
+  const uint8_t* np = nib + ((size_t)row * ng + g) * 16;
+  float* out = w + (size_t)row * ld + (size_t)g * 32;
+  for (int c = 0; c < 32; ++c) {
+    const int i = c & 15, half = c >> 4;
+    uint32_t q = half ? (np[i] >> 4) : (np[i] & 15u);
+    if (bits == 5) {
+      uint32_t hw = hb[(size_t)row * ng + g];
+      q |= ((hw >> c) & 1u) << 4;
+    } else if (bits == 6) {
+      q |= high_bits_crumb(hb + ((size_t)row * ng + g) * 2, i, half) << 4;
+    }
+    out[c] = (float)q * s + m;
+  }
+}
+
+__global__ void dq_sym(const uint8_t* codes, const uint32_t* hb,
+                       const int8_t* qsp, const uint16_t* dp, int bits,
+                       int rows, int in, float* w, int ld) {
+  const int ng = in >> 5, nsb = in >> 8;
+  long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (long)rows * ng) return;
+  const int row = (int)(t / ng), g = (int)(t % ng);
+  const float d = f16_bits_to_f32(dp[(size_t)row * nsb + (g >> 3)]);
+  const float sA = f16_round(((float)qsp[(size_t)row * (in >> 4) + 2 * g] * d));
+  const float sB = f16_round(((float)qsp[(size_t)row * (in >> 4) + 2 * g + 1] * d));
+  float* out = w + (size_t)row * ld + (size_t)g * 32;
+  for (int c = 0; c < 32; ++c) {
+    int q;
+    if (bits == 8) {
+      q = (int)(int8_t)codes[(size_t)row * in + (size_t)g * 32 + c];
+    } else {
+      // 16-block local split: byte j of block b holds columns j and j + 8
+      const int blk = c >> 4, cc = c & 15;
+      const int byte = blk * 8 + (cc & 7), half = cc >> 3;
+      const uint8_t v = codes[((size_t)row * ng + g) * 16 + byte];
+      uint32_t u = half ? (v >> 4) : (v & 15u);
+      u |= high_bits_crumb(hb + ((size_t)row * ng + g) * 2, byte, half) << 4;
+      q = (int)u - 32;
+    }
+    out[c] = (float)q * (c < 16 ? sA : sB);
+  }
+}
+
+__global__ void dq_rtn8(const int8_t* codes, const uint16_t* scale, int rows,
+                        int in, float* w, int ld) {
+  long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (long)rows * in) return;
+  const int row = (int)(t / in), c = (int)(t % in);
+  w[(size_t)row * ld + c] = (float)codes[t] * f16_bits_to_f32(scale[row]);
+}
+
+__global__ void dq_asym(const uint8_t* codes, const float* scale,
+                        const float* mn, int gs, int rows, int in, float* w,
+                        int ld) {
+  long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (long)rows * in) return;
+  const int row = (int)(t / in), c = (int)(t % in);
+  const int nb = (in + gs - 1) / gs;
+  const size_t b = (size_t)row * nb + c / gs;
+  w[(size_t)row * ld + c] = (float)codes[t] * scale[b] + mn[b];
+}
+
+inline dim3 grid_for(long n, int bs) { return dim3((unsigned)((n + bs - 1) / bs)); }
+
+}  // namespace
+
+extern "C" {
+
+int rwkvq_dequant_sb6_f32(const uint8_t* nib, const uint32_t* hb,
+                          const uint8_t* rec, int bits, int rows, int in,
+                          float* w, int ld, void* stream) {
+  if (rows <= 0 || in <= 0 || in % 256 || ld < in || bits < 4 || bits > 6 ||
+      (bits > 4 && !hb))
+    return RWKVQ_ERR_ARG;
+  long n = (long)rows * (in / 32);
+  hipLaunchKernelGGL(dq_sb6, grid_for(n, 256), dim3(256), 0,
+                     (hipStream_t)stream, nib, hb, rec, bits, rows, in, w, ld);
+  return hipGetLastError() == hipSuccess ? RWKVQ_OK : RWKVQ_ERR_LAUNCH;
+}
+
+int rwkvq_dequant_sym_f32(const uint8_t* codes, const uint32_t* hb,
+                          const int8_t* qs, const uint16_t* d, int bits,
+                          int rows, int in, float* w, int ld, void* stream) {
+  if (rows <= 0 || in <= 0 || in % 256 || ld < in || (bits != 6 && bits != 8) ||
+      (bits == 6 && !hb))
+    return RWKVQ_ERR_ARG;
+  long n = (long)rows * (in / 32);
+  hipLaunchKernelGGL(dq_sym, grid_for(n, 256), dim3(256), 0,
+                     (hipStream_t)stream, codes, hb, qs, d, bits, rows, in, w, ld);
+  return hipGetLastError() == hipSuccess ? RWKVQ_OK : RWKVQ_ERR_LAUNCH;
+}
+
+int rwkvq_dequant_rtn8_f32(const int8_t* codes, const uint16_t* scale,
+                           int rows, int in, float* w, int ld, void* stream) {
+  if (rows <= 0 || in <= 0 || ld < in) return RWKVQ_ERR_ARG;
+  long n = (long)rows * in;
+  hipLaunchKernelGGL(dq_rtn8, grid_for(n, 256), dim3(256), 0,
+                     (hipStream_t)stream, codes, scale, rows, in, w, ld);
+  return hipGetLastError() == hipSuccess ? RWKVQ_OK : RWKVQ_ERR_LAUNCH;
+}
+
+int rwkvq_dequant_asym_f32(const uint8_t* codes, const float* scale,
+                           const float* mn, int gs, int rows, int in,
+                           float* w, int ld, void* stream) {
+  if (rows <= 0 || in <= 0 || gs <= 0 || ld < in) return RWKVQ_ERR_ARG;
+  long n = (long)rows * in;
+  hipLaunchKernelGGL(dq_asym, grid_for(n, 256), dim3(256), 0,
+                     (hipStream_t)stream, codes, scale, mn, gs, rows, in, w, ld);
+  return hipGetLastError() == hipSuccess ? RWKVQ_OK : RWKVQ_ERR_LAUNCH;
+}
+
+}  // extern "C"

@@ -1,0 +1,81 @@
+// Shared device helpers for the gfx950 (CDNA4) kernels of librwkvq_hip.
+//
+// Wave64 everywhere: one wavefront = 64 lanes; reductions use DPP/permute
+// across the full wave.  No packed-fp32 instructions are written by hand.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "rwkvq_hip.h"
+
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+
+namespace rwkvq {
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t bits16) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+}
+
+// float32(float16(v)) with round-to-nearest-even, the fp16 round trip the
+// format uses for block scales.
+__device__ __forceinline__ float f16_round(float v) {
+  return (float)(_Float16)v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+  v += __shfl_xor(v, 32, 64);
+  v += __shfl_xor(v, 16, 64);
+  v += __shfl_xor(v, 8, 64);
+  v += __shfl_xor(v, 4, 64);
+  v += __shfl_xor(v, 2, 64);
+  v += __shfl_xor(v, 1, 64);
+  return v;
+}
+
+// 16-byte global load as four dwords.
+__device__ __forceinline__ uint4 ld16(const void* p) {
+  return *reinterpret_cast<const uint4*>(p);
+}
+
+// Nibble byte pair -> two fp16 lanes holding 1024 + code:
+// result low half = 0x6400 | (lo nibble of byte j of w) [| high bits],
+// high half = 0x6400 | (hi nibble of byte j of w).
+// `ws` must be w >> 4.  v_perm_b32 picks byte j of w and of ws, zeroing the
+// other two bytes; v_and_or_b32 keeps the nibbles and sets the exponent.
+template <int J>
+__device__ __forceinline__ uint32_t nib_pair(uint32_t w, uint32_t ws) {
+  constexpr uint32_t sel = (uint32_t)J | (0x0Cu << 8) | ((4u + J) << 16) |
+                           (0x0Cu << 24);
+  uint32_t t = __builtin_amdgcn_perm(ws, w, sel);
+  return (t & 0x000F000Fu) | 0x64006400u;
+}
+
+// Signed byte pair (bytes 2P, 2P+1 of w) -> two fp16 lanes holding
+// 1024 + 128 + code  (code in -128..127).
+template <int P>
+__device__ __forceinline__ uint32_t i8_pair(uint32_t w) {
+  constexpr uint32_t sel = (uint32_t)(2 * P) | (0x0Cu << 8) |
+                           ((uint32_t)(2 * P + 1) << 16) | (0x0Cu << 24);
+  uint32_t t = __builtin_amdgcn_perm(0u, w, sel);
+  return t ^ 0x64806480u;
+}
+
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_t, a),
+                                __builtin_bit_cast(h2_t, b), c, false);
+}
+
+__device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
+  _Float16 a = (_Float16)lo, b = (_Float16)hi;
+  return (uint32_t)__builtin_bit_cast(uint16_t, a) |
+         ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+
+__device__ __forceinline__ float h2_lo(uint32_t u) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(u & 0xFFFFu));
+}
+__device__ __forceinline__ float h2_hi(uint32_t u) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(u >> 16));
+}
+
+}  // namespace rwkvq

@@ -1,0 +1,75 @@
+"""ctypes binding of librwkvq_hip.so (the C ABI declared in
+include/rwkvq_hip.h).
+
+The library is built in-tree by `rwkv-quant_amd/build_hip.py`; there is no
+fallback: if it is missing or a call fails, an exception is raised.
+"""
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "librwkvq_hip.so")
+
+RWKVQ_OK = 0
+ERRORS = {1001: "invalid argument or shape", 1002: "kernel launch failed",
+          1003: "size beyond a supported limit"}
+
+EPI_STORE, EPI_ADD, EPI_RELU2, EPI_TANH, EPI_SIGMOID = 0, 1, 2, 3, 4
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_F = ctypes.c_float
+
+# name -> argument types (all return int status)
+SIGNATURES = {
+    "rwkvq_gemv_sb6": [_P, _P, _P, _I, _I, _I, _I, _P, _P, _I, _I, _P],
+    "rwkvq_gemv_sym": [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _I, _I, _P],
+    "rwkvq_gemv_rtn8": [_P, _P, _I, _I, _I, _P, _P, _I, _I, _P],
+    "rwkvq_dequant_sb6_f32": [_P, _P, _P, _I, _I, _I, _P, _I, _P],
+    "rwkvq_dequant_sym_f32": [_P, _P, _P, _P, _I, _I, _I, _P, _I, _P],
+    "rwkvq_dequant_rtn8_f32": [_P, _P, _I, _I, _P, _I, _P],
+    "rwkvq_dequant_asym_f32": [_P, _P, _P, _I, _I, _I, _P, _I, _P],
+}
+
+_lib = None
+
+
+class HipKernelError(RuntimeError):
+    pass
+
+
+def load():
+    """Load the library once; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise HipKernelError(
+            f"{LIB_PATH} is missing: build it with "
+            f"`python rwkv-quant_amd/build_hip.py` (hipcc, gfx950)")
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, argtypes in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        fn.restype = ctypes.c_int
+    _lib = lib
+    return lib
+
+
+def call(name, *args):
+    """Invoke an entry point; a non-zero status raises HipKernelError."""
+    st = getattr(load(), name)(*args)
+    if st != RWKVQ_OK:
+        raise HipKernelError(f"{name}: status {st} "
+                             f"({ERRORS.get(st, 'hip error')})")
+
+
+def ptr(t):
+    """Device pointer of a tensor (None -> NULL)."""
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def stream_handle(stream=None):
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)

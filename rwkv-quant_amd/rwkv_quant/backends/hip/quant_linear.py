@@ -1,0 +1,306 @@
+"""Quantized Linear layers of the HIP backend.
+
+Same contract as the reference Metal classes
+(reference: rwkv_quant/backends/metal/quant_linear_gw.py:747-1020,
+            rwkv_quant/backends/metal/quant_linear_sym.py:372-574,
+            rwkv_quant/backends/metal/quant_linear_v2.py:282-351):
+
+  Linear(qt)                   load-time repack of the canonical buffers
+                               into the device layout (memory 1x)
+  .in_features / .out_features
+  __call__(x [..., IN])        -> [..., OUT] float32 on the GPU
+  _dequant_w(dtype)            dense [OUT, IN] (float32 is bit-exact with
+                               the format's dequant)
+  Fused(lins)(xstack [K, IN])  -> [K, out_per]: the K row-concatenated
+                               matrices in one launch
+
+Batches of up to GEMM_MIN_BATCH_NB - 1 rows take the GEMV kernel (which
+reads each weight once per 4 rows); larger batches (prefill) take the GEMM
+path.  Every path runs a HIP kernel of librwkvq_hip; nothing here computes
+on the CPU.
+"""
+import numpy as np
+import torch
+
+from . import _lib
+from .repack import rtn8_device, sb6_device, sym_device
+
+GEMM_MIN_BATCH_NB = 128          # reference: quant_linear_gw.py:153
+NB_CHUNK = 4                     # rows per GEMV launch (kernel-internal)
+
+
+def _np(t):
+    return None if t is None else t.detach().cpu().contiguous().numpy()
+
+
+def _dev(a, device):
+    if a is None:
+        return None
+    return torch.from_numpy(np.ascontiguousarray(a)).to(device)
+
+
+def _flat_x(x, in_features):
+    if not x.is_cuda:
+        raise ValueError("HIP linear: input must be a GPU tensor")
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, in_features)
+    if x2.dtype != torch.float32:
+        x2 = x2.float()
+    return lead, x2.contiguous()
+
+
+class _HipLinearBase:
+    out_features: int
+    in_features: int
+    device: torch.device
+
+    def _gemv(self, x2, y, out_per=None, mode=_lib.EPI_STORE):
+        raise NotImplementedError
+
+    def __call__(self, x, mode=_lib.EPI_STORE):
+        lead, x2 = _flat_x(x, self.in_features)
+        n = x2.shape[0]
+        if n >= GEMM_MIN_BATCH_NB and mode == _lib.EPI_STORE:
+            y = self._gemm(x2)
+        else:
+            y = torch.empty((n, self.out_features), dtype=torch.float32,
+                            device=x2.device)
+            self._gemv(x2, y, mode=mode)
+        return y.reshape(*lead, self.out_features)
+
+    def gemv_into(self, x2, y, mode=_lib.EPI_STORE):
+        """y [N, OUT] (preallocated) <- epi(x2 [N, IN] @ W^T)."""
+        self._gemv(x2, y, mode=mode)
+        return y
+
+    def _gemm(self, x2):
+        # prefill: dense fp16 weights from the bit-exact dequant kernel,
+        # fp16 GEMM with fp32 output (reference: quant_linear_gw.py:846-849)
+        w = self._dequant_w(torch.float16)
+        return torch.matmul(x2.half(), w.t()).float()
+
+    def _dequant_w(self, dtype=torch.float16):
+        w = torch.empty((self.out_features, self.in_features),
+                        dtype=torch.float32, device=self.device)
+        self._dequant_into(w)
+        return w if dtype == torch.float32 else w.to(dtype)
+
+
+class GwQuantLinear(_HipLinearBase):
+    """sb6 tensor (gs 32, sb 8, bits 4/5/6)."""
+
+    def __init__(self, qt, device="cuda"):
+        assert qt.gw_mode == "sb6", qt.gw_mode
+        assert qt.gw_gs == 32 and qt.gw_sb == 8, (qt.gw_gs, qt.gw_sb)
+        self.out_features, self.in_features = qt.shape
+        self.bits = int(qt.bits)
+        self.xbits = self.bits - 4
+        self.has_qh = self.xbits >= 1
+        self.device = torch.device(device)
+        lay = sb6_device(_np(qt.codes_packed), _np(qt.gw_qsqm), _np(qt.gw_d),
+                         _np(qt.gw_dm), shape=qt.shape, bits=self.bits,
+                         qh=_np(qt.gw_qh), qh2=_np(qt.gw_qh2))
+        self._set(lay)
+
+    def _set(self, lay):
+        self.nib = _dev(lay["nib"], self.device)
+        self.hb = _dev(lay["hb"], self.device) if lay["hb"] is not None \
+            else None
+        self.rec = _dev(lay["rec"], self.device)
+
+    def _gemv(self, x2, y, out_per=None, mode=_lib.EPI_STORE):
+        _lib.call("rwkvq_gemv_sb6", _lib.ptr(self.nib), _lib.ptr(self.hb),
+                  _lib.ptr(self.rec), self.bits, self.out_features,
+                  self.in_features, out_per or self.out_features,
+                  _lib.ptr(x2), _lib.ptr(y), x2.shape[0] if out_per is None
+                  else x2.shape[0] // (self.out_features // out_per), mode,
+                  _lib.stream_handle())
+
+    def _dequant_into(self, w):
+        _lib.call("rwkvq_dequant_sb6_f32", _lib.ptr(self.nib),
+                  _lib.ptr(self.hb), _lib.ptr(self.rec), self.bits,
+                  self.out_features, self.in_features, _lib.ptr(w),
+                  self.in_features, _lib.stream_handle())
+
+
+class SymQuantLinear(_HipLinearBase):
+    """sym tensor (Q6_K style, gs 16, sb 16, bits 6/8)."""
+
+    def __init__(self, qt, device="cuda"):
+        assert qt.gw_mode == "sym", qt.gw_mode
+        assert qt.gw_gs == 16 and qt.gw_sb == 16, (qt.gw_gs, qt.gw_sb)
+        self._build(shape=qt.shape, bits=qt.bits, codes=_np(qt.codes),
+                    codes_packed=_np(qt.codes_packed), qh=_np(qt.gw_qh),
+                    qh2=_np(qt.gw_qh2), qs=_np(qt.gw_qs), d=_np(qt.gw_d),
+                    device=device)
+
+    @classmethod
+    def from_buffers(cls, *, shape, bits, qs, d, codes=None,
+                     codes_packed=None, qh=None, qh2=None, device="cuda"):
+        """Torch-free construction from numpy buffers
+        (reference: quant_linear_sym.py:392-405)."""
+        obj = cls.__new__(cls)
+        obj._build(shape=shape, bits=bits, codes=codes,
+                   codes_packed=codes_packed, qh=qh, qh2=qh2, qs=qs, d=d,
+                   device=device)
+        return obj
+
+    def _build(self, *, shape, bits, codes, codes_packed, qh, qh2, qs, d,
+               device):
+        self.out_features, self.in_features = shape
+        assert self.in_features % 256 == 0, \
+            f"sym kernel: IN={self.in_features} is not a multiple of 256"
+        self.bits = int(bits)
+        self.device = torch.device(device)
+        lay = sym_device(qs, d, shape=shape, bits=self.bits, codes=codes,
+                         codes_packed=codes_packed, qh=qh, qh2=qh2)
+        self.codes = _dev(lay["codes"], self.device)
+        self.hb = _dev(lay["hb"], self.device) if lay["hb"] is not None \
+            else None
+        self.qs = _dev(lay["qs"], self.device)
+        self.d = _dev(lay["d"].view(np.uint16), self.device)
+
+    def can_fuse_with(self, other):
+        return (self.bits == other.bits
+                and self.in_features == other.in_features
+                and self.out_features == other.out_features)
+
+    def _gemv(self, x2, y, out_per=None, mode=_lib.EPI_STORE):
+        k = 1 if out_per is None else self.out_features // out_per
+        _lib.call("rwkvq_gemv_sym", _lib.ptr(self.codes), _lib.ptr(self.hb),
+                  _lib.ptr(self.qs), _lib.ptr(self.d), self.bits,
+                  self.out_features, self.in_features,
+                  out_per or self.out_features, _lib.ptr(x2), _lib.ptr(y),
+                  x2.shape[0] // k, mode, _lib.stream_handle())
+
+    def _dequant_into(self, w):
+        _lib.call("rwkvq_dequant_sym_f32", _lib.ptr(self.codes),
+                  _lib.ptr(self.hb), _lib.ptr(self.qs), _lib.ptr(self.d),
+                  self.bits, self.out_features, self.in_features,
+                  _lib.ptr(w), self.in_features, _lib.stream_handle())
+
+
+class QuantLinearV2(_HipLinearBase):
+    """Per-row RTN int8 (+ optional SpQR outliers)."""
+
+    def __init__(self, qt, device="cuda"):
+        assert qt.bits < 16
+        if qt.codes is None:
+            raise NotImplementedError("HIP rtn kernel: packed int4 rtn is "
+                                      "not supported (no preset uses it)")
+        self.out_features, self.in_features = qt.shape
+        assert self.in_features % 256 == 0, \
+            f"rtn kernel: IN={self.in_features} is not a multiple of 256"
+        self.device = torch.device(device)
+        lay = rtn8_device(_np(qt.codes), _np(qt.scale), shape=qt.shape)
+        self.codes = _dev(lay["codes"], self.device)
+        self.scale = _dev(lay["scale"].view(np.uint16), self.device)
+        self.has_outliers = (qt.outlier_indices is not None
+                             and qt.outlier_indices.numel() > 0)
+        if self.has_outliers:
+            oi = qt.outlier_indices.long()
+            self._out_rows = oi[:, 0].to(self.device)
+            self._out_cols = oi[:, 1].to(self.device)
+            self._out_vals = qt.outlier_values.float().to(self.device)
+
+    def _gemv(self, x2, y, out_per=None, mode=_lib.EPI_STORE):
+        k = 1 if out_per is None else self.out_features // out_per
+        if self.has_outliers and mode != _lib.EPI_STORE:
+            raise NotImplementedError("outliers with a fused epilogue")
+        _lib.call("rwkvq_gemv_rtn8", _lib.ptr(self.codes),
+                  _lib.ptr(self.scale), self.out_features, self.in_features,
+                  out_per or self.out_features, _lib.ptr(x2), _lib.ptr(y),
+                  x2.shape[0] // k, mode, _lib.stream_handle())
+        if self.has_outliers:
+            # codes are 0 at outlier positions; add x[c] * value
+            y.index_add_(1, self._out_rows,
+                         x2[:, self._out_cols] * self._out_vals)
+
+    def _dequant_into(self, w):
+        _lib.call("rwkvq_dequant_rtn8_f32", _lib.ptr(self.codes),
+                  _lib.ptr(self.scale), self.out_features, self.in_features,
+                  _lib.ptr(w), self.in_features, _lib.stream_handle())
+        if self.has_outliers:
+            w[self._out_rows, self._out_cols] = self._out_vals
+
+
+class _FusedBase:
+    """K row-concatenated linears of one kind and shape, one launch."""
+
+    def __init__(self, lins, cls):
+        l0 = lins[0]
+        assert all(isinstance(l, cls) for l in lins)
+        assert all(l.in_features == l0.in_features
+                   and l.out_features == l0.out_features for l in lins)
+        self.K = len(lins)
+        self.out_per = l0.out_features
+        self.out_features = self.out_per * self.K
+        self.in_features = l0.in_features
+
+    def __call__(self, xstack, mode=_lib.EPI_STORE):
+        lead, x2 = _flat_x(xstack, self.in_features)
+        assert x2.shape[0] % self.K == 0
+        n = x2.shape[0] // self.K
+        y = torch.empty((n, self.out_features), dtype=torch.float32,
+                        device=x2.device)
+        self._cat._gemv(x2, y, out_per=self.out_per, mode=mode)
+        return y.reshape(n * self.K, self.out_per) if n > 1 else \
+            y.reshape(self.K, self.out_per)
+
+
+class GwQuantLinearFused(_FusedBase):
+    def __init__(self, lins):
+        super().__init__(lins, GwQuantLinear)
+        assert len({l.bits for l in lins}) == 1
+        cat = GwQuantLinear.__new__(GwQuantLinear)
+        cat.out_features, cat.in_features = self.out_features, self.in_features
+        cat.bits, cat.xbits, cat.has_qh = lins[0].bits, lins[0].xbits, \
+            lins[0].has_qh
+        cat.device = lins[0].device
+        cat.nib = torch.cat([l.nib for l in lins])
+        cat.hb = None if lins[0].hb is None else torch.cat([l.hb for l in lins])
+        cat.rec = torch.cat([l.rec for l in lins])
+        self._cat = cat
+        self.bits = cat.bits
+
+
+class SymQuantLinearFused(_FusedBase):
+    def __init__(self, lins):
+        super().__init__(lins, SymQuantLinear)
+        assert all(lins[0].can_fuse_with(l) for l in lins)
+        cat = SymQuantLinear.__new__(SymQuantLinear)
+        cat.out_features, cat.in_features = self.out_features, self.in_features
+        cat.bits, cat.device = lins[0].bits, lins[0].device
+        cat.codes = torch.cat([l.codes for l in lins])
+        cat.hb = None if lins[0].hb is None else torch.cat([l.hb for l in lins])
+        cat.qs = torch.cat([l.qs for l in lins])
+        cat.d = torch.cat([l.d for l in lins])
+        self._cat = cat
+        self.bits = cat.bits
+
+
+def make_linear(qt, device="cuda"):
+    """QuantizedTensor [out, in] -> HIP linear (reference: quant_model.py:245-262)."""
+    if qt.bits >= 16:
+        return DenseLinear(qt.dense.to(torch.float16), device)
+    if qt.gw_mode == "sb6":
+        return GwQuantLinear(qt, device)
+    if qt.gw_mode == "sym":
+        return SymQuantLinear(qt, device)
+    if qt.gw_mode == "":
+        return QuantLinearV2(qt, device)
+    raise NotImplementedError(f"HIP linear for gw_mode={qt.gw_mode!r}")
+
+
+class DenseLinear:
+    """Unquantized [out, in] weight kept in fp16 (reference: quant_model.py:202-210)."""
+
+    def __init__(self, w, device="cuda"):
+        self.w = w.to(device=device, dtype=torch.float16).contiguous()
+        self.out_features, self.in_features = self.w.shape
+        self.device = self.w.device
+
+    def __call__(self, x, mode=_lib.EPI_STORE):
+        lead, x2 = _flat_x(x, self.in_features)
+        y = torch.matmul(x2.half(), self.w.t()).float()
+        return y.reshape(*lead, self.out_features)

@@ -1,0 +1,116 @@
+"""GPU parity of the dequant and GEMV kernels against the CPU oracle.
+
+Bars: device dequant == oracle dequant bit for bit (fp32 bytes);
+GEMV relmax < 1e-3 against float64 x . dequant(W)^T (BASELINE tolerance,
+tighter than the reference's 3e-3 gate, tests/test_gw_kernel.py:29);
+fused r/k/v == three separate launches bit for bit."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import codec_ref as cr
+from rwkv_quant.backends.hip import _lib
+from rwkv_quant.backends.hip.quant_linear import (
+    GwQuantLinear, GwQuantLinearFused, QuantLinearV2, SymQuantLinear,
+    SymQuantLinearFused)
+
+from _util import act, qt_for, relmax, weights
+
+pytestmark = pytest.mark.gpu
+
+LIN = {"sb6": GwQuantLinear, "sym": SymQuantLinear, "rtn": QuantLinearV2}
+FORMATS = [("sb6", 4), ("sb6", 5), ("sb6", 6), ("sym", 6), ("sym", 8),
+           ("rtn", 8)]
+
+
+def _assert_same_bits(dev, ref):
+    a = np.ascontiguousarray(dev, np.float32).view(np.uint32)
+    b = np.ascontiguousarray(ref, np.float32).view(np.uint32)
+    bad = int((a != b).sum())
+    assert a.shape == b.shape and bad == 0, f"{bad} of {a.size} differ"
+
+
+def _w(rows, cols, seed, degenerate=False, outliers=0):
+    w = weights(rows, cols, seed=seed, outlier_cols=outliers)
+    if degenerate:
+        w[3] = 0.0
+        w[5] = 1e-9
+        w[6, :256] = 0.0
+    return w
+
+
+@pytest.mark.parametrize("kind,bits", FORMATS)
+@pytest.mark.parametrize("shape", [(64, 512), (40, 2560)])
+def test_dequant_bit_exact(kind, bits, shape):
+    print(f"dequant {kind}@{bits} {shape}", flush=True)
+    w = _w(*shape, seed=11, degenerate=True, outliers=3)
+    qt = qt_for(kind, bits, w)
+    lin = LIN[kind](qt)
+    dev = lin._dequant_w(torch.float32).cpu().numpy()
+    ref = cr.dequant_qt(qt)
+    _assert_same_bits(dev, ref)
+
+
+def test_dequant_asym_bit_exact():
+    w = weights(96, 2048, seed=5)
+    qt = qt_for("asym", 6, w)
+    out = torch.empty(96, 2048, device="cuda")
+    codes = qt.codes.cuda()
+    sc, mn = qt.gw_scale.cuda(), qt.gw_min.cuda()
+    _lib.call("rwkvq_dequant_asym_f32", _lib.ptr(codes), _lib.ptr(sc),
+              _lib.ptr(mn), 64, 96, 2048, _lib.ptr(out), 2048,
+              _lib.stream_handle())
+    ref = cr.dequant_qt(qt)
+    _assert_same_bits(out.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("kind,bits", FORMATS)
+@pytest.mark.parametrize("shape", [(2048, 2048), (8192, 2048), (2048, 8192),
+                                   (512, 2560)])
+@pytest.mark.parametrize("n", [1, 3, 8])
+def test_gemv_relmax(kind, bits, shape, n):
+    print(f"gemv {kind}@{bits} {shape} n={n}", flush=True)
+    w = _w(*shape, seed=shape[0] + bits, outliers=2)
+    qt = qt_for(kind, bits, w)
+    lin = LIN[kind](qt)
+    x = act(n, shape[1], seed=n)
+    y = lin(x.cuda()).cpu().numpy()
+    ref = cr.gemv_ref(x.numpy(), cr.dequant_qt(qt))
+    assert relmax(y, ref) < 1e-3
+    # degenerate-reference control: the check must be able to fail
+    assert relmax(y, ref * 1.01) > 1e-3
+
+
+@pytest.mark.parametrize("kind,bits", [("sb6", 5), ("sym", 8), ("sb6", 4)])
+def test_fused_rkv_equals_separate(kind, bits):
+    lins = [LIN[kind](qt_for(kind, bits, _w(2048, 2048, seed=s)))
+            for s in range(3)]
+    fused = (GwQuantLinearFused if kind == "sb6" else SymQuantLinearFused)(lins)
+    x = act(3, 2048, seed=7).cuda()
+    yf = fused(x)
+    ys = torch.stack([lins[i](x[i:i + 1])[0] for i in range(3)])
+    assert torch.equal(yf, ys)
+
+
+@pytest.mark.parametrize("mode", [_lib.EPI_ADD, _lib.EPI_RELU2, _lib.EPI_TANH,
+                                  _lib.EPI_SIGMOID])
+def test_gemv_epilogues(mode):
+    lin = GwQuantLinear(qt_for("sb6", 4, _w(1024, 2048, seed=3)))
+    x = act(2, 2048, seed=4).cuda()
+    base = torch.empty(2, 1024, device="cuda")
+    lin.gemv_into(x, base)
+    y0 = torch.randn(2, 1024, device="cuda")
+    y = y0.clone()
+    lin.gemv_into(x, y, mode=mode)
+    expect = {_lib.EPI_ADD: y0 + base, _lib.EPI_RELU2: torch.relu(base) ** 2,
+              _lib.EPI_TANH: torch.tanh(base),
+              _lib.EPI_SIGMOID: torch.sigmoid(base)}[mode]
+    assert torch.allclose(y, expect, rtol=1e-5, atol=1e-6)
+
+
+def test_shape_errors_raise():
+    lin = GwQuantLinear(qt_for("sb6", 4, _w(64, 512, seed=1)))
+    with pytest.raises(_lib.HipKernelError):
+        _lib.call("rwkvq_gemv_sb6", _lib.ptr(lin.nib), None,
+                  _lib.ptr(lin.rec), 4, 64, 500, 64, None, None, 1, 0,
+                  _lib.stream_handle())

@@ -1,0 +1,92 @@
+"""Host-side checks: the device repack is a bit-preserving permutation of
+the canonical fields, and librwkvq_hip.so exports every entry point that
+include/rwkvq_hip.h declares (no device call is made)."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+from rwkv_quant.backends.hip import _lib, repack
+from rwkv_quant.formats import codec
+
+from _util import qt_for, weights
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _unrepack_crumbs(hb, n_out, n_in, pairs):
+    ng = n_in // 32
+    b4 = np.zeros((n_out, ng, 32), np.uint8)
+    b5 = np.zeros((n_out, ng, 32), np.uint8)
+    for i, (lo, hi) in enumerate(pairs):
+        H = hb[:, :, i // 8]
+        ip = i % 8
+        b4[:, :, lo] = (H >> (2 * ip)) & 1
+        b5[:, :, lo] = (H >> (2 * ip + 1)) & 1
+        b4[:, :, hi] = (H >> (16 + 2 * ip)) & 1
+        b5[:, :, hi] = (H >> (17 + 2 * ip)) & 1
+    return (codec.pack_bitplane(b4.reshape(n_out, n_in)),
+            codec.pack_bitplane(b5.reshape(n_out, n_in)))
+
+
+@pytest.mark.parametrize("bits", [4, 5, 6])
+def test_sb6_repack_is_bit_preserving(bits):
+    w = weights(64, 512, seed=bits)
+    qt = qt_for("sb6", bits, w)
+    lay = repack.sb6_device(qt.codes_packed.numpy(), qt.gw_qsqm.numpy(),
+                            qt.gw_d.numpy(), qt.gw_dm.numpy(), shape=qt.shape,
+                            bits=bits,
+                            qh=None if qt.gw_qh is None else qt.gw_qh.numpy(),
+                            qh2=None if qt.gw_qh2 is None else qt.gw_qh2.numpy())
+    assert np.array_equal(lay["nib"].reshape(64, 256), qt.codes_packed.numpy())
+    rec = lay["rec"]
+    assert np.array_equal(rec[..., :12], qt.gw_qsqm.numpy())
+    assert np.array_equal(rec[..., 12:14].copy().view(np.float16)[..., 0],
+                          qt.gw_d.numpy())
+    assert np.array_equal(rec[..., 14:16].copy().view(np.float16)[..., 0],
+                          qt.gw_dm.numpy())
+    canon = sum(getattr(qt, f).numel() * getattr(qt, f).element_size()
+                for f in ("codes_packed", "gw_qsqm", "gw_d", "gw_dm", "gw_qh",
+                          "gw_qh2") if getattr(qt, f) is not None)
+    dev = sum(a.nbytes for a in lay.values() if a is not None)
+    assert canon == dev
+    if bits == 5:
+        assert np.array_equal(lay["hb"].view(np.uint8).reshape(64, 64),
+                              qt.gw_qh.numpy())
+    if bits == 6:
+        qh, qh2 = _unrepack_crumbs(lay["hb"], 64, 512, repack.SB6_PAIRS)
+        assert np.array_equal(qh, qt.gw_qh.numpy())
+        assert np.array_equal(qh2, qt.gw_qh2.numpy())
+
+
+def test_sym6_repack_is_bit_preserving():
+    w = weights(32, 768, seed=9)
+    qt = qt_for("sym", 6, w)
+    lay = repack.sym_device(qt.gw_qs.numpy(), qt.gw_d.numpy(), shape=qt.shape,
+                            bits=6, codes_packed=qt.codes_packed.numpy(),
+                            qh=qt.gw_qh.numpy(), qh2=qt.gw_qh2.numpy())
+    qh, qh2 = _unrepack_crumbs(lay["hb"], 32, 768, repack.SYM_PAIRS)
+    assert np.array_equal(qh, qt.gw_qh.numpy())
+    assert np.array_equal(qh2, qt.gw_qh2.numpy())
+    assert np.array_equal(lay["codes"].reshape(32, 384),
+                          qt.codes_packed.numpy())
+
+
+def _declared_symbols():
+    text = open(os.path.join(ROOT, "include", "rwkvq_hip.h")).read()
+    return sorted(set(re.findall(r"\bint\s+(rwkvq_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.fail(f"{_lib.LIB_PATH} not built")
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    syms = _declared_symbols()
+    assert len(syms) >= 7
+    for s in syms:
+        assert hasattr(lib, s), s
+    # every declared symbol has a ctypes signature and vice versa
+    assert set(syms) == set(_lib.SIGNATURES)
