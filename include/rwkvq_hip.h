@@ -51,10 +51,11 @@ extern "C" {
 
 /* ---------------------------------------------------------------- GEMV
  * y[n, r] = epi( sum_c x[n, r / out_per, c] * W[r, c] ),  n < n_cols.
- * x is fp32 [n_cols, rows / out_per, IN]; y is fp32 [n_cols, rows].
+ * x is fp32 with element (n, seg, c) at x[n * x_ld + seg * IN + c]
+ * (x_ld = 0 means packed: (rows / out_per) * IN); y is fp32 [n_cols, rows].
  * out_per == rows is the plain GEMV; out_per < rows runs K = rows/out_per
  * row-concatenated matrices with their own inputs in one launch (the fused
- * r/k/v projection).  IN % 256 == 0, IN <= 8192, out_per % 4 == 0.
+ * r/k/v projection).  IN % 256 == 0, IN <= 8192, out_per % 2 == 0.
  * Inputs are rounded to fp16 pairs; products and sums are fp32.
  *
  * Replaces:
@@ -70,14 +71,14 @@ extern "C" {
  */
 int rwkvq_gemv_sb6(const uint8_t* nib, const uint32_t* hb, const uint8_t* rec,
                    int bits, int rows, int in, int out_per, const float* x,
-                   float* y, int n_cols, int epilogue, void* stream);
+                   long x_ld, float* y, int n_cols, int epilogue, void* stream);
 int rwkvq_gemv_sym(const uint8_t* codes, const uint32_t* hb, const int8_t* qs,
                    const uint16_t* d, int bits, int rows, int in, int out_per,
-                   const float* x, float* y, int n_cols, int epilogue,
-                   void* stream);
+                   const float* x, long x_ld, float* y, int n_cols,
+                   int epilogue, void* stream);
 int rwkvq_gemv_rtn8(const int8_t* codes, const uint16_t* scale, int rows,
-                    int in, int out_per, const float* x, float* y, int n_cols,
-                    int epilogue, void* stream);
+                    int in, int out_per, const float* x, long x_ld, float* y,
+                    int n_cols, int epilogue, void* stream);
 
 /* ------------------------------------------------------ dequant to fp32
  * Bit-exact with the format's dequant formula: w = q * s + m with
@@ -103,6 +104,95 @@ int rwkvq_dequant_rtn8_f32(const int8_t* codes, const uint16_t* scale,
 int rwkvq_dequant_asym_f32(const uint8_t* codes, const float* scale,
                            const float* mn, int gs, int rows, int in,
                            float* w, int ld, void* stream);
+
+/* Row gather of a packed matrix into fp32 (the embedding lookup):
+ * out[o, :] = dequant(W)[min(max(idx[o], 0), src_rows - 1), :], o < n_idx.
+ * kind 0 = sb6 (q = nib, hb, aux0 = rec), 1 = sym (q = codes, hb,
+ * aux0 = qs, aux1 = d), 2 = rtn@8 (q = codes, aux1 = scale).  Values are
+ * bit-exact with the dequant entry points above.
+ * Replaces: the emb gather on the dense table
+ *   (reference: rwkv_quant/backends/metal/quant_model.py:853, 975). */
+int rwkvq_gather_rows_f32(int kind, int bits, const uint8_t* q,
+                          const uint32_t* hb, const void* aux0,
+                          const uint16_t* aux1, int src_rows, int in,
+                          const int64_t* idx, int n_idx, float* out,
+                          void* stream);
+
+/* ------------------------------------------------------- RWKV-7 blocks
+ * Row layer norm (two-pass mean/variance): y = (x - mean) / sqrt(var + eps)
+ * * w + b over rows of D (x and y may alias).
+ * Replaces: _layer_norm (reference: quant_model.py:281-284). */
+int rwkvq_layer_norm(const float* x, const float* w, const float* b, float* y,
+                     int rows, int D, float eps, void* stream);
+
+/* LN (eps 1e-5) + token shift + ncoef lerps for x [B, T, D]:
+ * out[(b*T+t), c, :] = xn + (shift - xn) * coef[c, :], shift = xn of the
+ * previous token or prev[b] (zeros if prev is NULL) at t = 0;
+ * new_prev[b] = xn of the last token (may be NULL).
+ * Replaces: _token_shift_stateful + the six lerps of the time mix and the
+ * one of the channel mix (reference: quant_model.py:292-301, 643-650,
+ * 803-809). */
+int rwkvq_shift_lerp(const float* x, const float* ln_w, const float* ln_b,
+                     const float* prev, const float* coef, int ncoef,
+                     float* out, float* new_prev, int B, int T, int D,
+                     void* stream);
+
+/* Per-channel WKV inputs from rkv [N, 3, D] and the LoRA outputs yw, ya,
+ * yv (NULL on layer 0) [N, D]: w = exp(-0.606531 * sigmoid(yw + w0)),
+ * a = sigmoid(ya + a0), kk = l2norm_head(k * k_k), k' = k (1 + (a-1) k_a),
+ * v' = v + (v_first - v) sigmoid(yv + v0) (layer 0: v_first = v);
+ * outputs w, k', v', a_wkv = -kk, b_wkv = kk * a, all [N, D].
+ * Replaces: reference quant_model.py:693-712. */
+int rwkvq_wkv_prep(const float* rkv, const float* yw, const float* ya,
+                   const float* yv, const float* w0, const float* a0,
+                   const float* v0, const float* k_k, const float* k_a,
+                   float* v_first, int layer0, float* w, float* kp, float* vp,
+                   float* a, float* b, int N, int D, int head_size,
+                   void* stream);
+
+/* WKV-7 recurrence over T tokens for B sequences, H heads of 64:
+ * S = S diag(w_t) + (S a_t) b_t^T + v_t k_t^T;  y_t = S r_t  (fp32).
+ * Inputs [B, T, H*64] with token stride ld (r: r_ld); state [B, H, 64, 64]
+ * (row = value index, column = key index) is read from state_in (or
+ * state_out when NULL) and the final state written to state_out;
+ * y [B, T, ...] with token stride y_ld.
+ * Replaces: rwkv_metal wkv7_infer / wkv7_train (reference call sites
+ * quant_model.py:118-125, 394, 714; math rwkv7_ref.py:236-255). */
+int rwkvq_wkv7_scan(const float* r, long r_ld, const float* w, const float* k,
+                    const float* v, const float* a, const float* b, long ld,
+                    const float* state_in, float* state_out, float* y,
+                    long y_ld, int B, int T, int H, int head_size,
+                    void* stream);
+
+/* Time-mix tail per head: out = ((GN(y) ln_w + ln_b) + (sum r k' r_k) v') g
+ * with a two-pass group norm (eps 64e-5); r is rkv[:, 0, :].
+ * Replaces: wkv_tail (reference: fused_tail.py:43-110) and the unfused
+ * group_norm + bonus (quant_model.py:269-278, 722-728). */
+int rwkvq_wkv_tail(const float* y, const float* rkv, const float* kp,
+                   const float* vp, const float* g, const float* r_k,
+                   const float* ln_w, const float* ln_b, float* out, int N,
+                   int D, int head_size, void* stream);
+
+/* Grouped dense-fp16 GEMV of up to 4 low-rank branches in one launch:
+ * y_j[n, r] = epi_j( sum_c x_j[n * x_ld_j + c] * W_j[r, c] ), n < N <= 8.
+ * in_j % 16 == 0 (and % 128 when in_j > 512).
+ * Replaces: QuantTMix._lora down/up products (reference:
+ * quant_model.py:462-526). */
+int rwkvq_lora_gemv(int n_jobs, const void* const* W, const float* const* x,
+                    const int* x_ld, float* const* y, const int* y_ld,
+                    const int* rows, const int* in, const int* epi, int N,
+                    void* stream);
+
+/* ------------------------------------------------------------- probes
+ * HBM read ceiling: stream `bytes` (multiple of 16) with 16-byte loads
+ * from n_blocks workgroups of 256 threads; out[n_blocks] receives a
+ * checksum per workgroup.  The measured rate is the roofline reference
+ * next to the 8 TB/s datasheet peak.
+ * Replaces: the reference's stream-read ceiling probe
+ *   (reference: tests/bench_membw.py; NEXT_SESSION.md:2961-2996).
+ */
+int rwkvq_probe_stream_read(const void* buf, long bytes, uint32_t* out,
+                            int n_blocks, void* stream);
 
 #ifdef __cplusplus
 }

@@ -24,10 +24,10 @@ FLAGS = [
 ]
 
 
-def build(verbose=True):
+def build(verbose=True, out=OUT, defines=()):
     srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
-    tmp = OUT + ".tmp"
-    cmd = ["hipcc", *FLAGS, *srcs, "-o", tmp]
+    tmp = out + ".tmp"
+    cmd = ["hipcc", *FLAGS, *[f"-D{d}" for d in defines], *srcs, "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -37,10 +37,15 @@ def build(verbose=True):
         raise RuntimeError(f"hipcc failed ({r.returncode}):\n{err}")
     if err.strip() and verbose:
         print(err)
-    os.replace(tmp, OUT)
-    return OUT
+    os.replace(tmp, out)
+    return out
 
 
 if __name__ == "__main__":
-    print(build())
+    import argparse
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--out", default=OUT)
+    ap.add_argument("-D", dest="defines", action="append", default=[])
+    a = ap.parse_args()
+    print(build(out=a.out, defines=a.defines))
     sys.exit(0)

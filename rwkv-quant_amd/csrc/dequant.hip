@@ -23,13 +23,23 @@ __device__ __forceinline__ uint32_t high_bits_crumb(const uint32_t* hw, int i,
   return (H >> sh) & 3u;
 }
 
+// `idx` (optional) gathers rows: output row o is source row
+// min(idx[o], src_rows - 1) -- the embedding lookup.
+__device__ __forceinline__ int src_row(const int64_t* idx, int o,
+                                       int src_rows) {
+  if (!idx) return o;
+  long v = idx[o];
+  return (int)(v < 0 ? 0 : (v >= src_rows ? src_rows - 1 : v));
+}
+
 __global__ void dq_sb6(const uint8_t* nib, const uint32_t* hb,
                        const uint8_t* rec, int bits, int rows, int in,
-                       float* w, int ld) {
+                       float* w, int ld, const int64_t* idx, int src_rows) {
   const int ng = in >> 5, nsb = in >> 8;
   long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= (long)rows * ng) return;
-  const int row = (int)(t / ng), g = (int)(t % ng);
+  const int orow = (int)(t / ng), g = (int)(t % ng);
+  const int row = src_row(idx, orow, src_rows);
   const uint8_t* rp = rec + ((size_t)row * nsb + (g >> 3)) * 16;
   const int kb = g & 7;
   // 6-bit fields of the 48-bit qs stream and the 48-bit qm stream
@@ -45,7 +55,7 @@ __global__ void dq_sb6(const uint8_t* nib, const uint32_t* hb,
   const float s = fmaxf(f16_round(((float)qs * d)), 1e-8f);
   const float m = f16_round(((float)qm * dm));
   const uint8_t* np = nib + ((size_t)row * ng + g) * 16;
-  float* out = w + (size_t)row * ld + (size_t)g * 32;
+  float* out = w + (size_t)orow * ld + (size_t)g * 32;
   for (int c = 0; c < 32; ++c) {
     const int i = c & 15, half = c >> 4;
     uint32_t q = half ? (np[i] >> 4) : (np[i] & 15u);
@@ -61,15 +71,17 @@ __global__ void dq_sb6(const uint8_t* nib, const uint32_t* hb,
 
 __global__ void dq_sym(const uint8_t* codes, const uint32_t* hb,
                        const int8_t* qsp, const uint16_t* dp, int bits,
-                       int rows, int in, float* w, int ld) {
+                       int rows, int in, float* w, int ld, const int64_t* idx,
+                       int src_rows) {
   const int ng = in >> 5, nsb = in >> 8;
   long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= (long)rows * ng) return;
-  const int row = (int)(t / ng), g = (int)(t % ng);
+  const int orow = (int)(t / ng), g = (int)(t % ng);
+  const int row = src_row(idx, orow, src_rows);
   const float d = f16_bits_to_f32(dp[(size_t)row * nsb + (g >> 3)]);
   const float sA = f16_round(((float)qsp[(size_t)row * (in >> 4) + 2 * g] * d));
   const float sB = f16_round(((float)qsp[(size_t)row * (in >> 4) + 2 * g + 1] * d));
-  float* out = w + (size_t)row * ld + (size_t)g * 32;
+  float* out = w + (size_t)orow * ld + (size_t)g * 32;
   for (int c = 0; c < 32; ++c) {
     int q;
     if (bits == 8) {
@@ -88,11 +100,14 @@ __global__ void dq_sym(const uint8_t* codes, const uint32_t* hb,
 }
 
 __global__ void dq_rtn8(const int8_t* codes, const uint16_t* scale, int rows,
-                        int in, float* w, int ld) {
+                        int in, float* w, int ld, const int64_t* idx,
+                        int src_rows) {
   long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= (long)rows * in) return;
-  const int row = (int)(t / in), c = (int)(t % in);
-  w[(size_t)row * ld + c] = (float)codes[t] * f16_bits_to_f32(scale[row]);
+  const int orow = (int)(t / in), c = (int)(t % in);
+  const int row = src_row(idx, orow, src_rows);
+  w[(size_t)orow * ld + c] =
+      (float)codes[(size_t)row * in + c] * f16_bits_to_f32(scale[row]);
 }
 
 __global__ void dq_asym(const uint8_t* codes, const float* scale,
@@ -120,7 +135,8 @@ int rwkvq_dequant_sb6_f32(const uint8_t* nib, const uint32_t* hb,
     return RWKVQ_ERR_ARG;
   long n = (long)rows * (in / 32);
   hipLaunchKernelGGL(dq_sb6, grid_for(n, 256), dim3(256), 0,
-                     (hipStream_t)stream, nib, hb, rec, bits, rows, in, w, ld);
+                     (hipStream_t)stream, nib, hb, rec, bits, rows, in, w, ld,
+                     (const int64_t*)nullptr, rows);
   return hipGetLastError() == hipSuccess ? RWKVQ_OK : RWKVQ_ERR_LAUNCH;
 }
 
@@ -132,7 +148,8 @@ int rwkvq_dequant_sym_f32(const uint8_t* codes, const uint32_t* hb,
     return RWKVQ_ERR_ARG;
   long n = (long)rows * (in / 32);
   hipLaunchKernelGGL(dq_sym, grid_for(n, 256), dim3(256), 0,
-                     (hipStream_t)stream, codes, hb, qs, d, bits, rows, in, w, ld);
+                     (hipStream_t)stream, codes, hb, qs, d, bits, rows, in, w, ld,
+                     (const int64_t*)nullptr, rows);
   return hipGetLastError() == hipSuccess ? RWKVQ_OK : RWKVQ_ERR_LAUNCH;
 }
 
@@ -141,7 +158,8 @@ int rwkvq_dequant_rtn8_f32(const int8_t* codes, const uint16_t* scale,
   if (rows <= 0 || in <= 0 || ld < in) return RWKVQ_ERR_ARG;
   long n = (long)rows * in;
   hipLaunchKernelGGL(dq_rtn8, grid_for(n, 256), dim3(256), 0,
-                     (hipStream_t)stream, codes, scale, rows, in, w, ld);
+                     (hipStream_t)stream, codes, scale, rows, in, w, ld,
+                     (const int64_t*)nullptr, rows);
   return hipGetLastError() == hipSuccess ? RWKVQ_OK : RWKVQ_ERR_LAUNCH;
 }
 
@@ -152,6 +170,38 @@ int rwkvq_dequant_asym_f32(const uint8_t* codes, const float* scale,
   long n = (long)rows * in;
   hipLaunchKernelGGL(dq_asym, grid_for(n, 256), dim3(256), 0,
                      (hipStream_t)stream, codes, scale, mn, gs, rows, in, w, ld);
+  return hipGetLastError() == hipSuccess ? RWKVQ_OK : RWKVQ_ERR_LAUNCH;
+}
+
+int rwkvq_gather_rows_f32(int kind, int bits, const uint8_t* q,
+                          const uint32_t* hb, const void* aux0,
+                          const uint16_t* aux1, int src_rows, int in,
+                          const int64_t* idx, int n_idx, float* out,
+                          void* stream) {
+  if (n_idx <= 0 || src_rows <= 0 || in <= 0 || !idx) return RWKVQ_ERR_ARG;
+  hipStream_t s = (hipStream_t)stream;
+  if (kind == 0) {            // sb6: aux0 = rec
+    if (in % 256 || bits < 4 || bits > 6 || (bits > 4 && !hb))
+      return RWKVQ_ERR_ARG;
+    long n = (long)n_idx * (in / 32);
+    hipLaunchKernelGGL(dq_sb6, grid_for(n, 256), dim3(256), 0, s, q, hb,
+                       (const uint8_t*)aux0, bits, n_idx, in, out, in, idx,
+                       src_rows);
+  } else if (kind == 1) {     // sym: aux0 = qs, aux1 = d
+    if (in % 256 || (bits != 6 && bits != 8) || (bits == 6 && !hb))
+      return RWKVQ_ERR_ARG;
+    long n = (long)n_idx * (in / 32);
+    hipLaunchKernelGGL(dq_sym, grid_for(n, 256), dim3(256), 0, s, q, hb,
+                       (const int8_t*)aux0, aux1, bits, n_idx, in, out, in,
+                       idx, src_rows);
+  } else if (kind == 2) {     // rtn@8: aux1 = scale
+    long n = (long)n_idx * in;
+    hipLaunchKernelGGL(dq_rtn8, grid_for(n, 256), dim3(256), 0, s,
+                       (const int8_t*)q, aux1, n_idx, in, out, in, idx,
+                       src_rows);
+  } else {
+    return RWKVQ_ERR_ARG;
+  }
   return hipGetLastError() == hipSuccess ? RWKVQ_OK : RWKVQ_ERR_LAUNCH;
 }
 

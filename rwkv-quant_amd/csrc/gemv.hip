@@ -38,8 +38,9 @@ struct GemvArgs {
   const uint8_t* rec;    // sb6 superblock records [rows, NSB, 16]
   const int8_t* qs;      // sym block-scale codes [rows, IN/16]
   const uint16_t* d;     // sym: f16 d [rows, NSB]; rtn: f16 row scale [rows]
-  const float* x;        // [N, n_seg, IN]
+  const float* x;        // x[n * x_ld + seg * IN + c]
   float* y;              // [N, rows]
+  long x_ld;
   int rows, in, out_per, n_seg, ks, rg, rpw, mode, n;
 };
 
@@ -57,14 +58,44 @@ __device__ __forceinline__ float magic_bias() {
   return 1152.0f;                       // 1024 + 128 (signed byte bias)
 }
 
-// Decode one (row, group) into 16 fp16 pairs.
+// Raw bytes of one (row, group): issued as loads one row batch ahead of
+// the arithmetic that consumes them.
+struct Raw {
+  uint4 a;        // nibbles, or codes 0..15 (int8 formats)
+  uint4 b;        // sb6 superblock record, or codes 16..31 (int8 formats)
+  uint2 h;        // high-bit words
+  uint32_t s;     // sym: qs pair (low 16 bits) | d (high 16 bits)
+};
+
 template <int FMT>
-__device__ __forceinline__ void decode_group(const GemvArgs& a, size_t row,
-                                             int ng, int g, uint32_t h[16]) {
+__device__ __forceinline__ void load_raw(const GemvArgs& a, int row, int ng,
+                                         int nsb, int g, Raw& r) {
   if (FMT == F_SYM8 || FMT == F_RTN8) {
-    const uint8_t* p = a.q + row * (size_t)a.in + (size_t)g * 32;
-    uint4 u0 = ld16(p), u1 = ld16(p + 16);
-    uint32_t w[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+    const uint8_t* p = a.q + (size_t)row * a.in;     // wave-uniform
+    r.a = ld16(p + g * 32);
+    r.b = ld16(p + g * 32 + 16);
+  } else {
+    const uint8_t* p = a.q + (size_t)row * ng * 16;  // wave-uniform
+    r.a = ld16(p + g * 16);
+  }
+  if (FMT <= F_SB6_6)
+    r.b = ld16(a.rec + (size_t)row * nsb * 16 + (g >> 3) * 16);
+  if (FMT == F_SB6_5) r.h.x = a.hb[(size_t)row * ng + g];
+  if (FMT == F_SB6_6 || FMT == F_SYM6)
+    r.h = *reinterpret_cast<const uint2*>(a.hb + (size_t)row * ng * 2 + g * 2);
+  if (FMT == F_SYM6 || FMT == F_SYM8) {
+    uint32_t q2 = *reinterpret_cast<const uint16_t*>(
+        a.qs + (size_t)row * (a.in >> 4) + 2 * g);
+    uint32_t dd = a.d[(size_t)row * nsb + (g >> 3)];
+    r.s = q2 | (dd << 16);
+  }
+}
+
+// Raw bytes -> 16 fp16 pairs (1024 + code, offset by the storage bias).
+template <int FMT>
+__device__ __forceinline__ void decode_raw(const Raw& r, uint32_t h[16]) {
+  if (FMT == F_SYM8 || FMT == F_RTN8) {
+    uint32_t w[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       h[2 * k] = i8_pair<0>(w[k]);
@@ -72,8 +103,7 @@ __device__ __forceinline__ void decode_group(const GemvArgs& a, size_t row,
     }
     return;
   }
-  uint4 u = ld16(a.q + (row * ng + g) * 16);
-  uint32_t w[4] = {u.x, u.y, u.z, u.w};
+  uint32_t w[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     uint32_t ws = w[k] >> 4;
@@ -83,16 +113,15 @@ __device__ __forceinline__ void decode_group(const GemvArgs& a, size_t row,
     h[4 * k + 3] = nib_pair<3>(w[k], ws);
   }
   if (FMT == F_SB6_5) {
-    uint32_t hw = a.hb[row * ng + g];
+    uint32_t hw = r.h.x;
 #pragma unroll
     for (int i = 0; i < 16; ++i)
       h[i] |= __builtin_amdgcn_alignbit(hw, hw, (uint32_t)((i - 4) & 31)) &
               0x00100010u;
   } else if (FMT == F_SB6_6 || FMT == F_SYM6) {
-    uint2 hw = *reinterpret_cast<const uint2*>(a.hb + (row * ng + g) * 2);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      uint32_t H = (i < 8) ? hw.x : hw.y;
+      uint32_t H = (i < 8) ? r.h.x : r.h.y;
       int ip = i & 7;
       h[i] |= __builtin_amdgcn_alignbit(H, H, (uint32_t)((2 * ip - 4) & 31)) &
               0x00300030u;
@@ -104,32 +133,47 @@ template <int FMT, int NN, int RS>
 __global__ void __launch_bounds__(256)
 gemv_kernel(GemvArgs a) {
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  // wave-uniform values live in SGPRs: row addressing becomes scalar and
+  // only the lane's group offset is a VGPR
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int kslice = wave % a.ks;
   const int rgi = wave / a.ks;
   const int ng = a.in >> 5;
   const int g = kslice * 64 + lane;
   const bool active = g < ng;
+  const int gl = active ? g : 0;               // in-bounds group for loads
   const int row_base = (blockIdx.x * a.rg + rgi) * a.rpw;
   const int nsb = a.in >> 8;
 
-  __shared__ float red[4 * 4 * RS * NN];   // [wave][RS*NN], waves <= 4*?
-  // (max 16 waves of 64 = 1024 threads is not used; launch caps at 256)
+  __shared__ float red[4 * RS * NN];
+
+  // first weight batch in flight before x is fetched: the two HBM round
+  // trips overlap instead of adding up.  Loads are unconditional (row index
+  // clamped into the matrix) so the compiler can count them and wait only
+  // for the batch it consumes.
+  const int nrows = min(a.rpw, a.rows - row_base);   // rows of this wave
+  const int last = a.rows - 1;
+  Raw cur[RS], nxt[RS];
+#pragma unroll
+  for (int j = 0; j < RS; ++j)
+    load_raw<FMT>(a, min(row_base + j, last), ng, nsb, gl, cur[j]);
 
   // ---- lane-resident x: 16 fp16 pairs per column + block sums
-  int seg = row_base < a.rows ? row_base / a.out_per : 0;
+  const int seg = row_base < a.rows ? row_base / a.out_per : 0;
   uint32_t xh[NN][16];
   float xsa[NN], xsb[NN], xsf[NN];
 #pragma unroll
   for (int n = 0; n < NN; ++n) {
     float sa = 0.f, sb = 0.f, sf = 0.f;
     if (active && n < a.n) {
-      const float* xp = a.x + ((size_t)n * a.n_seg + seg) * a.in + (size_t)g * 32;
+      const float* xp =
+          a.x + (size_t)n * a.x_ld + (size_t)seg * a.in + (size_t)g * 32;
       float xv[32];
 #pragma unroll
       for (int t = 0; t < 8; ++t) {
         float4 f = reinterpret_cast<const float4*>(xp)[t];
-        xv[4 * t] = f.x; xv[4 * t + 1] = f.y; xv[4 * t + 2] = f.z; xv[4 * t + 3] = f.w;
+        xv[4 * t] = f.x; xv[4 * t + 1] = f.y;
+        xv[4 * t + 2] = f.z; xv[4 * t + 3] = f.w;
       }
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
@@ -137,8 +181,8 @@ gemv_kernel(GemvArgs a) {
         x_cols<FMT>(i, c0, c1);
         uint32_t p = pack_h2(xv[c0], xv[c1]);
         xh[n][i] = p;
-        float s = h2_lo(p) + h2_hi(p);
-        if (i < 8) sa += s; else sb += s;
+        float s2 = h2_lo(p) + h2_hi(p);
+        if (i < 8) sa += s2; else sb += s2;
       }
 #pragma unroll
       for (int c = 0; c < 32; ++c) sf += xv[c];
@@ -146,29 +190,31 @@ gemv_kernel(GemvArgs a) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) xh[n][i] = 0u;
     }
-    xsa[n] = sa; xsb[n] = sb; xsf[n] = sf;
+    const float mb = magic_bias<FMT>();
+    xsa[n] = -mb * sa; xsb[n] = -mb * sb; xsf[n] = sf;
   }
 
   // per-lane constants for sb6 scale extraction (block k of its superblock)
   const int kb = g & 7;
   const int qs_word = (6 * kb) >> 5, qs_sh = (6 * kb) & 31;
   const int qm_word = (48 + 6 * kb) >> 5, qm_sh = (48 + 6 * kb) & 31;
-  const float mb = magic_bias<FMT>();
+
 
   for (int r0 = 0; r0 < a.rpw; r0 += RS) {
+    // prefetch the next batch before touching this one
+#pragma unroll
+    for (int j = 0; j < RS; ++j)
+      load_raw<FMT>(a, min(row_base + r0 + RS + j, last), ng, nsb, gl, nxt[j]);
+
     float acc[NN][RS];
 #pragma unroll
     for (int j = 0; j < RS; ++j) {
-      const int row = row_base + r0 + j;
-#pragma unroll
-      for (int n = 0; n < NN; ++n) acc[n][j] = 0.f;
-      if (!active || row >= a.rows) continue;
       uint32_t h[16];
-      decode_group<FMT>(a, (size_t)row, ng, g, h);
+      decode_raw<FMT>(cur[j], h);
       float dA[NN], dB[NN];
 #pragma unroll
       for (int n = 0; n < NN; ++n) {
-        float ca = -mb * xsa[n], cb = -mb * xsb[n];
+        float ca = xsa[n], cb = xsb[n];
 #pragma unroll
         for (int i = 0; i < 8; ++i) ca = dot2(h[i], xh[n][i], ca);
 #pragma unroll
@@ -176,38 +222,38 @@ gemv_kernel(GemvArgs a) {
         dA[n] = ca; dB[n] = cb;
       }
       if (FMT <= F_SB6_6) {
-        uint4 rc = ld16(a.rec + ((size_t)row * nsb + (g >> 3)) * 16);
-        uint32_t r[4] = {rc.x, rc.y, rc.z, rc.w};
-        uint32_t lo = qs_word == 0 ? r[0] : r[1];
-        uint32_t hi = qs_word == 0 ? r[1] : r[2];
+        const uint32_t rr[4] = {cur[j].b.x, cur[j].b.y, cur[j].b.z,
+                                cur[j].b.w};
+        uint32_t lo = qs_word == 0 ? rr[0] : rr[1];
+        uint32_t hi = qs_word == 0 ? rr[1] : rr[2];
         uint32_t qsv = __builtin_amdgcn_alignbit(hi, lo, (uint32_t)qs_sh) & 63u;
-        lo = qm_word == 1 ? r[1] : r[2];
-        hi = qm_word == 1 ? r[2] : r[3];
+        lo = qm_word == 1 ? rr[1] : rr[2];
+        hi = qm_word == 1 ? rr[2] : rr[3];
         uint32_t qmv = __builtin_amdgcn_alignbit(hi, lo, (uint32_t)qm_sh) & 63u;
-        float d = f16_bits_to_f32(r[3] & 0xFFFFu);
-        float dm = f16_bits_to_f32(r[3] >> 16);
+        float d = f16_bits_to_f32(rr[3] & 0xFFFFu);
+        float dm = f16_bits_to_f32(rr[3] >> 16);
         float s = fmaxf(f16_round((float)qsv * d), 1e-8f);
         float m = f16_round((float)((int)qmv - 31) * dm);
 #pragma unroll
-        for (int n = 0; n < NN; ++n) acc[n][j] = s * (dA[n] + dB[n]) + m * xsf[n];
+        for (int n = 0; n < NN; ++n)
+          acc[n][j] = active ? s * (dA[n] + dB[n]) + m * xsf[n] : 0.f;
       } else if (FMT == F_SYM6 || FMT == F_SYM8) {
-        uint32_t q2 = *reinterpret_cast<const uint16_t*>(
-            a.qs + (size_t)row * (a.in >> 4) + 2 * g);
-        float d = f16_bits_to_f32(a.d[(size_t)row * nsb + (g >> 3)]);
-        float sA = f16_round((float)(int8_t)(q2 & 0xFFu) * d);
-        float sB = f16_round((float)(int8_t)(q2 >> 8) * d);
+        float d = f16_bits_to_f32(cur[j].s >> 16);
+        float sA = f16_round((float)(int8_t)(cur[j].s & 0xFFu) * d);
+        float sB = f16_round((float)(int8_t)((cur[j].s >> 8) & 0xFFu) * d);
 #pragma unroll
-        for (int n = 0; n < NN; ++n) acc[n][j] = sA * dA[n] + sB * dB[n];
+        for (int n = 0; n < NN; ++n)
+          acc[n][j] = active ? sA * dA[n] + sB * dB[n] : 0.f;
       } else {
 #pragma unroll
-        for (int n = 0; n < NN; ++n) acc[n][j] = dA[n] + dB[n];
+        for (int n = 0; n < NN; ++n) acc[n][j] = active ? dA[n] + dB[n] : 0.f;
       }
     }
-    // ---- reduce over the 64 lanes, then over K-slices through LDS
+    // ---- reduce over the 64 lanes (uniform result), then K-slices in LDS
 #pragma unroll
     for (int n = 0; n < NN; ++n)
 #pragma unroll
-      for (int j = 0; j < RS; ++j) acc[n][j] = wave_sum(acc[n][j]);
+      for (int j = 0; j < RS; ++j) acc[n][j] = wave_sum_dpp(acc[n][j]);
     if (a.ks > 1) {
       if (lane == 0) {
 #pragma unroll
@@ -221,22 +267,22 @@ gemv_kernel(GemvArgs a) {
         for (int n = 0; n < NN; ++n)
 #pragma unroll
           for (int j = 0; j < RS; ++j) {
-            float s = 0.f;
+            float s2 = 0.f;
             for (int k = 0; k < a.ks; ++k)
-              s += red[((wave + k) * NN + n) * RS + j];
-            acc[n][j] = s;
+              s2 += red[((wave + k) * NN + n) * RS + j];
+            acc[n][j] = s2;
           }
       }
       __syncthreads();
     }
-    if (kslice == 0 && lane < RS) {
+    if (kslice == 0 && lane < RS * NN) {
+      // lane (n * RS + j) writes row r0 + j of column n
 #pragma unroll
-      for (int j = 0; j < RS; ++j) {
-        const int row = row_base + r0 + j;
-        if (j != lane || row >= a.rows) continue;
+      for (int n = 0; n < NN; ++n)
 #pragma unroll
-        for (int n = 0; n < NN; ++n) {
-          if (n >= a.n) continue;
+        for (int j = 0; j < RS; ++j) {
+          const int row = row_base + r0 + j;
+          if (lane != n * RS + j || n >= a.n || r0 + j >= nrows) continue;
           float v = acc[n][j];
           if (FMT == F_RTN8) v *= f16_bits_to_f32(a.d[row]);
           float* yp = a.y + (size_t)n * a.rows + row;
@@ -249,16 +295,46 @@ gemv_kernel(GemvArgs a) {
           }
           *yp = v;
         }
-      }
     }
+#pragma unroll
+    for (int j = 0; j < RS; ++j) cur[j] = nxt[j];
   }
 }
 
-constexpr int kRS = 4;
+#ifndef RWKVQ_TARGET_WAVES
+#define RWKVQ_TARGET_WAVES 4096
+#endif
+#ifndef RWKVQ_MAX_RPW
+#define RWKVQ_MAX_RPW 32
+#endif
 
-template <int FMT, int NN>
-void launch_nn(const GemvArgs& a, dim3 grid, dim3 block, hipStream_t s) {
-  hipLaunchKernelGGL((gemv_kernel<FMT, NN, kRS>), grid, block, 0, s, a);
+template <int FMT, int RS>
+int launch_rs(GemvArgs a, hipStream_t s) {
+  // rows per wave: aim for RWKVQ_TARGET_WAVES waves, at least RS rows; a
+  // wave's rows share one x segment
+  long rows_waves = (long)a.rows * a.ks;
+  int rpw = (int)(rows_waves / RWKVQ_TARGET_WAVES);
+  rpw = rpw < RS ? RS : (rpw / RS) * RS;
+  if (rpw > RWKVQ_MAX_RPW) rpw = RWKVQ_MAX_RPW;
+  while (rpw > RS && a.out_per % rpw) rpw -= RS;
+  if (a.out_per % rpw) return RWKVQ_ERR_ARG;
+  a.rpw = rpw;
+  const int rows_per_wg = a.rg * rpw;
+  dim3 grid((a.rows + rows_per_wg - 1) / rows_per_wg);
+  dim3 block(64 * a.ks * a.rg);
+  for (int n0 = 0; n0 < a.n; n0 += 4) {
+    GemvArgs b = a;
+    b.x = a.x + (size_t)n0 * a.x_ld;
+    b.y = a.y + (size_t)n0 * a.rows;
+    b.n = a.n - n0 < 4 ? a.n - n0 : 4;
+    switch (b.n) {
+      case 1: hipLaunchKernelGGL((gemv_kernel<FMT, 1, RS>), grid, block, 0, s, b); break;
+      case 2: hipLaunchKernelGGL((gemv_kernel<FMT, 2, RS>), grid, block, 0, s, b); break;
+      case 3: hipLaunchKernelGGL((gemv_kernel<FMT, 3, RS>), grid, block, 0, s, b); break;
+      default: hipLaunchKernelGGL((gemv_kernel<FMT, 4, RS>), grid, block, 0, s, b); break;
+    }
+  }
+  return hipGetLastError() == hipSuccess ? RWKVQ_OK : RWKVQ_ERR_LAUNCH;
 }
 
 template <int FMT>
@@ -268,38 +344,19 @@ int launch_fmt(GemvArgs a, hipStream_t s) {
   if (a.ks > 4) return RWKVQ_ERR_SIZE;          // IN > 8192 not tiled here
   a.rg = 4 / a.ks;
   if (a.rg < 1) a.rg = 1;
-  const int waves = a.ks * a.rg;
-  // rows per wave: aim for >= 2048 waves in flight, at least kRS rows
-  long rows_waves = (long)a.rows * a.ks;
-  int rpw = (int)(rows_waves / 4096);
-  rpw = rpw < kRS ? kRS : (rpw / kRS) * kRS;
-  if (rpw > 32) rpw = 32;
-  // a wave's rows share one x segment
-  while (a.out_per % rpw) rpw -= kRS;
-  if (rpw < kRS) return RWKVQ_ERR_ARG;
-  a.rpw = rpw;
-  const int rows_per_wg = a.rg * rpw;
-  dim3 grid((a.rows + rows_per_wg - 1) / rows_per_wg);
-  dim3 block(64 * waves);
-  for (int n0 = 0; n0 < a.n; n0 += 4) {
-    GemvArgs b = a;
-    b.x = a.x + (size_t)n0 * a.n_seg * a.in;
-    b.y = a.y + (size_t)n0 * a.rows;
-    b.n = a.n - n0 < 4 ? a.n - n0 : 4;
-    switch (b.n) {
-      case 1: launch_nn<FMT, 1>(b, grid, block, s); break;
-      case 2: launch_nn<FMT, 2>(b, grid, block, s); break;
-      case 3: launch_nn<FMT, 3>(b, grid, block, s); break;
-      default: launch_nn<FMT, 4>(b, grid, block, s); break;
-    }
-  }
-  return hipGetLastError() == hipSuccess ? RWKVQ_OK : RWKVQ_ERR_LAUNCH;
+  // small matrices: 2-row batches keep more waves in flight; large ones
+  // amortise the lane-resident x over 4-row batches
+  if ((long)a.rows * a.ks <= 8192 && a.out_per % 4 != 0)
+    return launch_rs<FMT, 2>(a, s);
+  if ((long)a.rows * a.ks <= 8192) return launch_rs<FMT, 2>(a, s);
+  if (a.out_per % 4) return launch_rs<FMT, 2>(a, s);
+  return launch_rs<FMT, 4>(a, s);
 }
 
 int check_common(int rows, int in, int out_per, int n, int mode) {
   if (rows <= 0 || in <= 0 || n <= 0 || out_per <= 0) return RWKVQ_ERR_ARG;
   if (in % 256) return RWKVQ_ERR_ARG;
-  if (rows % out_per || out_per % 4) return RWKVQ_ERR_ARG;
+  if (rows % out_per || out_per % 2) return RWKVQ_ERR_ARG;
   if (mode < 0 || mode > RWKVQ_EPI_SIGMOID) return RWKVQ_ERR_ARG;
   return RWKVQ_OK;
 }
@@ -310,7 +367,7 @@ extern "C" {
 
 int rwkvq_gemv_sb6(const uint8_t* nib, const uint32_t* hb, const uint8_t* rec,
                    int bits, int rows, int in, int out_per, const float* x,
-                   float* y, int n, int mode, void* stream) {
+                   long x_ld, float* y, int n, int mode, void* stream) {
   int st = check_common(rows, in, out_per, n, mode);
   if (st) return st;
   if (bits < 4 || bits > 6 || (bits > 4 && !hb)) return RWKVQ_ERR_ARG;
@@ -318,6 +375,8 @@ int rwkvq_gemv_sb6(const uint8_t* nib, const uint32_t* hb, const uint8_t* rec,
   a.q = nib; a.hb = hb; a.rec = rec; a.x = x; a.y = y;
   a.rows = rows; a.in = in; a.out_per = out_per; a.n_seg = rows / out_per;
   a.mode = mode; a.n = n;
+  a.x_ld = x_ld > 0 ? x_ld : (long)a.n_seg * in;
+  if (a.x_ld < (long)a.n_seg * in) return RWKVQ_ERR_ARG;
   hipStream_t s = (hipStream_t)stream;
   if (bits == 4) return launch_fmt<F_SB6_4>(a, s);
   if (bits == 5) return launch_fmt<F_SB6_5>(a, s);
@@ -326,7 +385,8 @@ int rwkvq_gemv_sb6(const uint8_t* nib, const uint32_t* hb, const uint8_t* rec,
 
 int rwkvq_gemv_sym(const uint8_t* codes, const uint32_t* hb, const int8_t* qs,
                    const uint16_t* d, int bits, int rows, int in, int out_per,
-                   const float* x, float* y, int n, int mode, void* stream) {
+                   const float* x, long x_ld, float* y, int n, int mode,
+                   void* stream) {
   int st = check_common(rows, in, out_per, n, mode);
   if (st) return st;
   if ((bits != 6 && bits != 8) || (bits == 6 && !hb)) return RWKVQ_ERR_ARG;
@@ -334,19 +394,23 @@ int rwkvq_gemv_sym(const uint8_t* codes, const uint32_t* hb, const int8_t* qs,
   a.q = codes; a.hb = hb; a.qs = qs; a.d = d; a.x = x; a.y = y;
   a.rows = rows; a.in = in; a.out_per = out_per; a.n_seg = rows / out_per;
   a.mode = mode; a.n = n;
+  a.x_ld = x_ld > 0 ? x_ld : (long)a.n_seg * in;
+  if (a.x_ld < (long)a.n_seg * in) return RWKVQ_ERR_ARG;
   hipStream_t s = (hipStream_t)stream;
   return bits == 6 ? launch_fmt<F_SYM6>(a, s) : launch_fmt<F_SYM8>(a, s);
 }
 
 int rwkvq_gemv_rtn8(const int8_t* codes, const uint16_t* scale, int rows,
-                    int in, int out_per, const float* x, float* y, int n,
-                    int mode, void* stream) {
+                    int in, int out_per, const float* x, long x_ld, float* y,
+                    int n, int mode, void* stream) {
   int st = check_common(rows, in, out_per, n, mode);
   if (st) return st;
   GemvArgs a{};
   a.q = reinterpret_cast<const uint8_t*>(codes); a.d = scale; a.x = x; a.y = y;
   a.rows = rows; a.in = in; a.out_per = out_per; a.n_seg = rows / out_per;
   a.mode = mode; a.n = n;
+  a.x_ld = x_ld > 0 ? x_ld : (long)a.n_seg * in;
+  if (a.x_ld < (long)a.n_seg * in) return RWKVQ_ERR_ARG;
   return launch_fmt<F_RTN8>(a, (hipStream_t)stream);
 }
 

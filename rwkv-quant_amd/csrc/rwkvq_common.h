@@ -22,6 +22,31 @@ __device__ __forceinline__ float f16_round(float v) {
   return (float)(_Float16)v;
 }
 
+// DPP move of a float within rows of 16 lanes (bound_ctrl: out-of-row
+// sources read 0, never used by the patterns below).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                         0xF, 0xF, true));
+}
+
+// Sum over all 64 lanes, result uniform (in every lane).  Butterflies
+// inside each 16-lane row with DPP (quad_perm xor1, xor2, row_half_mirror,
+// row_mirror), then the four row sums through v_readlane.
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += dpp_f<0xB1>(v);    // quad_perm [1,0,3,2]
+  v += dpp_f<0x4E>(v);    // quad_perm [2,3,0,1]
+  v += dpp_f<0x141>(v);   // row_half_mirror
+  v += dpp_f<0x140>(v);   // row_mirror
+  const int b = __builtin_bit_cast(int, v);
+  float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+  float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+  float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
+  float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
   v += __shfl_xor(v, 32, 64);
   v += __shfl_xor(v, 16, 64);

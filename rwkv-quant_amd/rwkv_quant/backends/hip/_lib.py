@@ -8,7 +8,8 @@ import ctypes
 import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "librwkvq_hip.so")
+LIB_PATH = os.environ.get("RWKVQ_HIP_LIB",
+                          os.path.join(_HERE, "librwkvq_hip.so"))
 
 RWKVQ_OK = 0
 ERRORS = {1001: "invalid argument or shape", 1002: "kernel launch failed",
@@ -19,16 +20,29 @@ EPI_STORE, EPI_ADD, EPI_RELU2, EPI_TANH, EPI_SIGMOID = 0, 1, 2, 3, 4
 _P = ctypes.c_void_p
 _I = ctypes.c_int
 _F = ctypes.c_float
+_L = ctypes.c_long
 
 # name -> argument types (all return int status)
 SIGNATURES = {
-    "rwkvq_gemv_sb6": [_P, _P, _P, _I, _I, _I, _I, _P, _P, _I, _I, _P],
-    "rwkvq_gemv_sym": [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _I, _I, _P],
-    "rwkvq_gemv_rtn8": [_P, _P, _I, _I, _I, _P, _P, _I, _I, _P],
+    "rwkvq_gemv_sb6": [_P, _P, _P, _I, _I, _I, _I, _P, _L, _P, _I, _I, _P],
+    "rwkvq_gemv_sym": [_P, _P, _P, _P, _I, _I, _I, _I, _P, _L, _P, _I, _I,
+                       _P],
+    "rwkvq_gemv_rtn8": [_P, _P, _I, _I, _I, _P, _L, _P, _I, _I, _P],
     "rwkvq_dequant_sb6_f32": [_P, _P, _P, _I, _I, _I, _P, _I, _P],
     "rwkvq_dequant_sym_f32": [_P, _P, _P, _P, _I, _I, _I, _P, _I, _P],
     "rwkvq_dequant_rtn8_f32": [_P, _P, _I, _I, _P, _I, _P],
     "rwkvq_dequant_asym_f32": [_P, _P, _P, _I, _I, _I, _P, _I, _P],
+    "rwkvq_probe_stream_read": [_P, ctypes.c_long, _P, _I, _P],
+    "rwkvq_gather_rows_f32": [_I, _I, _P, _P, _P, _P, _I, _I, _P, _I, _P,
+                              _P],
+    "rwkvq_layer_norm": [_P, _P, _P, _P, _I, _I, _F, _P],
+    "rwkvq_shift_lerp": [_P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _P],
+    "rwkvq_wkv_prep": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P,
+                       _P, _P, _P, _I, _I, _I, _P],
+    "rwkvq_wkv7_scan": [_P, _L, _P, _P, _P, _P, _P, _L, _P, _P, _P, _L, _I,
+                        _I, _I, _I, _P],
+    "rwkvq_wkv_tail": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P],
+    "rwkvq_lora_gemv": [_I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P],
 }
 
 _lib = None

@@ -54,7 +54,8 @@ class _HipLinearBase:
     in_features: int
     device: torch.device
 
-    def _gemv(self, x2, y, out_per=None, mode=_lib.EPI_STORE):
+    def _gemv(self, x2, y, out_per=None, mode=_lib.EPI_STORE, n=None,
+              x_ld=0):
         raise NotImplementedError
 
     def __call__(self, x, mode=_lib.EPI_STORE):
@@ -68,9 +69,11 @@ class _HipLinearBase:
             self._gemv(x2, y, mode=mode)
         return y.reshape(*lead, self.out_features)
 
-    def gemv_into(self, x2, y, mode=_lib.EPI_STORE):
-        """y [N, OUT] (preallocated) <- epi(x2 [N, IN] @ W^T)."""
-        self._gemv(x2, y, mode=mode)
+    def gemv_into(self, x2, y, mode=_lib.EPI_STORE, n=None, x_ld=0):
+        """y [N, OUT] (preallocated) <- epi(x2 [N, IN] @ W^T).  With x_ld,
+        row n of the input starts at element n * x_ld of x2 (a strided
+        view); n is then the number of rows."""
+        self._gemv(x2, y, mode=mode, n=n, x_ld=x_ld)
         return y
 
     def _gemm(self, x2):
@@ -108,12 +111,14 @@ class GwQuantLinear(_HipLinearBase):
             else None
         self.rec = _dev(lay["rec"], self.device)
 
-    def _gemv(self, x2, y, out_per=None, mode=_lib.EPI_STORE):
+    def _gemv(self, x2, y, out_per=None, mode=_lib.EPI_STORE, n=None,
+              x_ld=0):
+        k = 1 if out_per is None else self.out_features // out_per
         _lib.call("rwkvq_gemv_sb6", _lib.ptr(self.nib), _lib.ptr(self.hb),
                   _lib.ptr(self.rec), self.bits, self.out_features,
                   self.in_features, out_per or self.out_features,
-                  _lib.ptr(x2), _lib.ptr(y), x2.shape[0] if out_per is None
-                  else x2.shape[0] // (self.out_features // out_per), mode,
+                  _lib.ptr(x2), x_ld, _lib.ptr(y),
+                  n if n is not None else x2.shape[0] // k, mode,
                   _lib.stream_handle())
 
     def _dequant_into(self, w):
@@ -165,13 +170,15 @@ class SymQuantLinear(_HipLinearBase):
                 and self.in_features == other.in_features
                 and self.out_features == other.out_features)
 
-    def _gemv(self, x2, y, out_per=None, mode=_lib.EPI_STORE):
+    def _gemv(self, x2, y, out_per=None, mode=_lib.EPI_STORE, n=None,
+              x_ld=0):
         k = 1 if out_per is None else self.out_features // out_per
         _lib.call("rwkvq_gemv_sym", _lib.ptr(self.codes), _lib.ptr(self.hb),
                   _lib.ptr(self.qs), _lib.ptr(self.d), self.bits,
                   self.out_features, self.in_features,
-                  out_per or self.out_features, _lib.ptr(x2), _lib.ptr(y),
-                  x2.shape[0] // k, mode, _lib.stream_handle())
+                  out_per or self.out_features, _lib.ptr(x2), x_ld,
+                  _lib.ptr(y), n if n is not None else x2.shape[0] // k,
+                  mode, _lib.stream_handle())
 
     def _dequant_into(self, w):
         _lib.call("rwkvq_dequant_sym_f32", _lib.ptr(self.codes),
@@ -203,14 +210,16 @@ class QuantLinearV2(_HipLinearBase):
             self._out_cols = oi[:, 1].to(self.device)
             self._out_vals = qt.outlier_values.float().to(self.device)
 
-    def _gemv(self, x2, y, out_per=None, mode=_lib.EPI_STORE):
+    def _gemv(self, x2, y, out_per=None, mode=_lib.EPI_STORE, n=None,
+              x_ld=0):
         k = 1 if out_per is None else self.out_features // out_per
-        if self.has_outliers and mode != _lib.EPI_STORE:
+        if self.has_outliers and (mode != _lib.EPI_STORE or x_ld):
             raise NotImplementedError("outliers with a fused epilogue")
         _lib.call("rwkvq_gemv_rtn8", _lib.ptr(self.codes),
                   _lib.ptr(self.scale), self.out_features, self.in_features,
-                  out_per or self.out_features, _lib.ptr(x2), _lib.ptr(y),
-                  x2.shape[0] // k, mode, _lib.stream_handle())
+                  out_per or self.out_features, _lib.ptr(x2), x_ld,
+                  _lib.ptr(y), n if n is not None else x2.shape[0] // k,
+                  mode, _lib.stream_handle())
         if self.has_outliers:
             # codes are 0 at outlier positions; add x[c] * value
             y.index_add_(1, self._out_rows,
@@ -236,6 +245,13 @@ class _FusedBase:
         self.out_per = l0.out_features
         self.out_features = self.out_per * self.K
         self.in_features = l0.in_features
+
+    def gemv_into(self, x, y, n, x_ld, mode=_lib.EPI_STORE):
+        """y [n, K * out_per] <- the K matrices applied to their own inputs:
+        input (row t, matrix k) starts at element t * x_ld + k * IN of x."""
+        self._cat._gemv(x, y, out_per=self.out_per, mode=mode, n=n,
+                        x_ld=x_ld)
+        return y
 
     def __call__(self, xstack, mode=_lib.EPI_STORE):
         lead, x2 = _flat_x(xstack, self.in_features)

@@ -1,0 +1,519 @@
+"""RWKV-7 x070 inference on a `.rwkvq` checkpoint through the HIP kernels.
+
+Same interface as the reference Metal model
+(reference: rwkv_quant/backends/metal/quant_model.py:838-990):
+
+    model = QuantRWKV7(ckpt)                 # QuantizedCheckpoint
+    states = model.init_state(B)
+    logits, states = model.forward_stateful(idx[B, T], states,
+                                            last_only=False, tail_only=0)
+    logits, states = model.step(idx, states)  # decode: HIP-graph replay
+    hidden, states = model.forward_hidden(idx, states)
+    logits = model(idx)
+
+State per layer: (wkv [B, H, N, N] fp32, time-mix shift [B, 1, D] or None,
+channel-mix shift [B, 1, D] or None), None meaning a zero shift on the
+first call (reference: quant_model.py:902-908).  Tensors live on the GPU.
+
+Execution per layer (every numeric step is a librwkvq_hip kernel):
+  shift_lerp(ln1, 6 lerps) -> fused r/k/v GEMV (one launch) ->
+  LoRA down (4 branches, one launch) -> LoRA up (one launch) ->
+  wkv_prep -> wkv7_scan -> wkv_tail -> o_proj GEMV (+= residual) ->
+  shift_lerp(ln2, 1 lerp) -> key GEMV (relu^2) -> value GEMV (+= residual)
+Prefill (B*T >= GEMM_MIN_BATCH_NB) runs the projections as fp16 GEMMs on
+device-dequantized weights and the LoRA products as fp16 GEMMs.
+
+Runtime switches (module attributes, as the reference's FUSE flags):
+  FUSE        fuse r/k/v into one GEMV launch at decode
+  USE_GRAPH   replay decode steps from a captured HIP graph
+"""
+import ctypes
+
+import torch
+
+from . import _lib
+from .quant_linear import (GEMM_MIN_BATCH_NB, DenseLinear, GwQuantLinear,
+                           GwQuantLinearFused, QuantLinearV2, SymQuantLinear,
+                           SymQuantLinearFused, make_linear)
+
+FUSE = True
+USE_GRAPH = True
+LORA_KERNEL_MAX_N = 8          # rows handled by the grouped LoRA kernel
+
+_LORA = ("w1", "w2", "a1", "a2", "v1", "v2", "g1", "g2")
+
+
+def _stream():
+    return _lib.stream_handle()
+
+
+def dense_param(qt, device):
+    """QuantizedTensor -> exact float32 device tensor in stored orientation.
+    Quantized tensors are expanded by the bit-exact dequant kernels."""
+    shape = tuple(qt.shape)
+    if qt.bits >= 16:
+        return qt.dense.to(device=device, dtype=torch.float32).reshape(shape)
+    rows = shape[0]
+    cols = 1
+    for s in shape[1:]:
+        cols *= s
+    out = torch.empty((rows, cols), dtype=torch.float32, device=device)
+    if qt.gw_mode == "asym":
+        codes = qt.codes.to(device).view(torch.uint8).contiguous()
+        sc = qt.gw_scale.to(device).float().contiguous()
+        mn = qt.gw_min.to(device).float().contiguous()
+        _lib.call("rwkvq_dequant_asym_f32", _lib.ptr(codes), _lib.ptr(sc),
+                  _lib.ptr(mn), qt.gw_gs, rows, cols, _lib.ptr(out), cols,
+                  _stream())
+    elif qt.gw_mode == "" and qt.codes is not None and qt.bits <= 8:
+        codes = qt.codes.to(device).view(torch.int8).reshape(rows, cols) \
+            .contiguous()
+        sc = qt.scale.to(device).view(torch.int16).reshape(rows).contiguous()
+        _lib.call("rwkvq_dequant_rtn8_f32", _lib.ptr(codes), _lib.ptr(sc),
+                  rows, cols, _lib.ptr(out), cols, _stream())
+        if qt.outlier_indices is not None and qt.outlier_indices.numel():
+            oi = qt.outlier_indices.long().to(device)
+            out[oi[:, 0], oi[:, 1]] = qt.outlier_values.float().to(device)
+    elif qt.gw_mode in ("sb6", "sym") or qt.gw_mode == "":
+        lin = make_linear(qt, device)
+        lin._dequant_into(out)
+    else:
+        raise NotImplementedError(f"dense_param: {qt.gw_mode!r}")
+    return out.reshape(shape)
+
+
+class EmbTable:
+    """Token embedding: row gather straight from the packed table."""
+
+    def __init__(self, qt, device):
+        self.vocab, self.dim = qt.shape
+        self.device = device
+        self.dense = None
+        if qt.bits >= 16:
+            self.dense = qt.dense.to(device=device, dtype=torch.float32)
+            return
+        self.lin = make_linear(qt, device)
+        if isinstance(self.lin, GwQuantLinear):
+            self.kind, self.bits = 0, self.lin.bits
+            self.args = (self.lin.nib, self.lin.hb, self.lin.rec, None)
+        elif isinstance(self.lin, SymQuantLinear):
+            self.kind, self.bits = 1, self.lin.bits
+            self.args = (self.lin.codes, self.lin.hb, self.lin.qs, self.lin.d)
+        elif isinstance(self.lin, QuantLinearV2):
+            if self.lin.has_outliers:
+                raise NotImplementedError("rtn emb with outliers")
+            self.kind, self.bits = 2, 8
+            self.args = (self.lin.codes, None, None, self.lin.scale)
+        else:
+            raise NotImplementedError(type(self.lin))
+
+    def gather_into(self, idx, out):
+        """idx int64 [n] on device -> out [n, D] fp32."""
+        if self.dense is not None:
+            torch.index_select(self.dense, 0, idx, out=out)
+            return out
+        q, hb, a0, a1 = self.args
+        _lib.call("rwkvq_gather_rows_f32", self.kind, self.bits, _lib.ptr(q),
+                  _lib.ptr(hb), _lib.ptr(a0), _lib.ptr(a1), self.vocab,
+                  self.dim, _lib.ptr(idx), idx.numel(), _lib.ptr(out),
+                  _stream())
+        return out
+
+
+class _Work:
+    """Activation buffers for N = B*T rows (reused across layers)."""
+
+    def __init__(self, N, C, ffn, ranks, device):
+        f = dict(dtype=torch.float32, device=device)
+        self.N = N
+        self.x = torch.empty(N, C, **f)          # residual stream
+        self.xs = torch.empty(N, 6, C, **f)      # r, k, v, w, a, g lerps
+        self.rkv = torch.empty(N, 3, C, **f)
+        self.h = {b: torch.empty(N, r, **f) for b, r in ranks.items()}
+        self.yl = {b: torch.empty(N, C, **f) for b in ranks}
+        self.w = torch.empty(N, C, **f)
+        self.kp = torch.empty(N, C, **f)
+        self.vp = torch.empty(N, C, **f)
+        self.aa = torch.empty(N, C, **f)
+        self.bb = torch.empty(N, C, **f)
+        self.y = torch.empty(N, C, **f)
+        self.o = torch.empty(N, C, **f)
+        self.v_first = torch.empty(N, C, **f)
+        self.xk = torch.empty(N, C, **f)
+        self.hk = torch.empty(N, ffn, **f)
+        self.xo = torch.empty(N, C, **f)
+
+
+class QuantTMix:
+    def __init__(self, tensors, prefix, naming, layer_id, n_head, head_size,
+                 device):
+        self.H, self.S, self.layer_id = n_head, head_size, layer_id
+        g = lambda s: tensors[prefix + s]
+        dev = device
+        if naming == "world":
+            names = dict(x=["x_r", "x_k", "x_v", "x_w", "x_a", "x_g"],
+                         r="receptance.weight", k="key.weight",
+                         v="value.weight", o="output.weight",
+                         w0="w0", a0="a0", v0="v0")
+            pre = "att."
+
+            def lora(nm, up):
+                t = dense_param(g(pre + nm), dev)
+                return t.t().contiguous()        # stored [in, out]
+        else:
+            names = dict(x=["x_r", "x_k", "x_v", "x_w", "x_a", "x_g"],
+                         r="r_proj.weight", k="k_proj.weight",
+                         v="v_proj.weight", o="o_proj.weight",
+                         w0="w_lora_B.bias", a0="a_lora_B.bias",
+                         v0="v_lora_B.bias")
+            pre = "tmix."
+            custom = {"w1": "w_lora_A.weight", "w2": "w_lora_B.weight",
+                      "a1": "a_lora_A.weight", "a2": "a_lora_B.weight",
+                      "v1": "v_lora_A.weight", "v2": "v_lora_B.weight",
+                      "g1": "g_lora_A.weight", "g2": "g_lora_B.weight"}
+
+            def lora(nm, up):
+                return dense_param(g(pre + custom[nm]), dev)
+        vec = lambda s: dense_param(g(pre + s), dev).reshape(-1).contiguous()
+        # lerp coefficients in kernel order r, k, v, w, a, g
+        self.coef = torch.stack([vec(s) for s in names["x"]]).contiguous()
+        C = self.coef.shape[1]
+        self.C = C
+        self.r_proj = make_linear(g(pre + names["r"]), dev)
+        self.k_proj = make_linear(g(pre + names["k"]), dev)
+        self.v_proj = make_linear(g(pre + names["v"]), dev)
+        self.o_proj = make_linear(g(pre + names["o"]), dev)
+        self.w0 = vec(names["w0"])
+        self.a0 = vec(names["a0"])
+        self.v0 = vec(names["v0"]) if layer_id > 0 else None
+        self.k_k, self.k_a, self.r_k = vec("k_k"), vec("k_a"), vec("r_k")
+        self.ln_x_w, self.ln_x_b = vec("ln_x.weight"), vec("ln_x.bias")
+        # LoRA: A [r, C] (down), B [C, r] (up), fp16 on device
+        self.lora = {}
+        for b in ("w", "a", "v", "g"):
+            if b == "v" and layer_id == 0:
+                continue
+            A = lora(b + "1", False).to(torch.float16).contiguous()
+            Bm = lora(b + "2", True).to(torch.float16).contiguous()
+            self.lora[b] = (A, Bm)
+        self.rkv_fused = None
+        lins = [self.r_proj, self.k_proj, self.v_proj]
+        if all(isinstance(l, GwQuantLinear) for l in lins) and \
+                len({(l.in_features, l.out_features, l.bits)
+                     for l in lins}) == 1:
+            self.rkv_fused = GwQuantLinearFused(lins)
+        elif all(isinstance(l, SymQuantLinear) for l in lins) and \
+                all(lins[0].can_fuse_with(l) for l in lins):
+            self.rkv_fused = SymQuantLinearFused(lins)
+
+    # order of the lerp slots in work.xs
+    SLOT = {"r": 0, "k": 1, "v": 2, "w": 3, "a": 4, "g": 5}
+    EPI_DOWN = {"w": _lib.EPI_TANH, "a": _lib.EPI_STORE, "v": _lib.EPI_STORE,
+                "g": _lib.EPI_SIGMOID}
+
+    def run_lora(self, wk):
+        N, C = wk.N, self.C
+        branches = list(self.lora)
+        if N <= LORA_KERNEL_MAX_N:
+            xs_flat = wk.xs.view(N, 6 * C)
+            W = [self.lora[b][0] for b in branches]
+            X = [xs_flat[:, self.SLOT[b] * C:] for b in branches]
+            self._grouped(W, X, [6 * C] * len(branches),
+                          [wk.h[b] for b in branches],
+                          [self.EPI_DOWN[b] for b in branches], N)
+            W = [self.lora[b][1] for b in branches]
+            X = [wk.h[b] for b in branches]
+            self._grouped(W, X, [wk.h[b].shape[1] for b in branches],
+                          [wk.yl[b] for b in branches],
+                          [_lib.EPI_STORE] * len(branches), N)
+            return
+        for b in branches:
+            A, Bm = self.lora[b]
+            h = torch.matmul(wk.xs[:, self.SLOT[b]].half(), A.t()).float()
+            if b == "w":
+                h = torch.tanh(h)
+            elif b == "g":
+                h = torch.sigmoid(h)
+            wk.yl[b].copy_(torch.matmul(h.half(), Bm.t()).float())
+
+    @staticmethod
+    def _grouped(W, X, x_ld, Y, epi, N):
+        """One rwkvq_lora_gemv launch over the branches (host arrays of
+        pointers and sizes; the kernel receives them by value)."""
+        n = len(W)
+        vp = (ctypes.c_void_p * n)(*[w.data_ptr() for w in W])
+        xp = (ctypes.c_void_p * n)(*[x.data_ptr() for x in X])
+        yp = (ctypes.c_void_p * n)(*[y.data_ptr() for y in Y])
+        ia = lambda v: (ctypes.c_int * n)(*v)
+        _lib.call("rwkvq_lora_gemv", n, vp, xp, ia(x_ld), yp,
+                  ia([y.shape[1] for y in Y]), ia([w.shape[0] for w in W]),
+                  ia([w.shape[1] for w in W]), ia(epi), N, _stream())
+
+
+class QuantCMix:
+    def __init__(self, tensors, prefix, naming, device):
+        pre = "cmix." if naming == "custom" else "ffn."
+        g = lambda s: tensors[prefix + pre + s]
+        self.x_k = dense_param(g("x_k"), device).reshape(1, -1).contiguous()
+        self.key = make_linear(g("key.weight"), device)
+        self.value = make_linear(g("value.weight"), device)
+
+
+class QuantBlock:
+    def __init__(self, tensors, prefix, naming, layer_id, n_head, head_size,
+                 device):
+        vec = lambda s: dense_param(tensors[prefix + s], device).reshape(-1) \
+            .contiguous()
+        self.ln1_w, self.ln1_b = vec("ln1.weight"), vec("ln1.bias")
+        self.ln2_w, self.ln2_b = vec("ln2.weight"), vec("ln2.bias")
+        self.tmix = QuantTMix(tensors, prefix, naming, layer_id, n_head,
+                              head_size, device)
+        self.cmix = QuantCMix(tensors, prefix, naming, device)
+
+
+def _apply(lin, x2, y, mode, n=None, x_ld=0):
+    """y <- epi(x2 @ W^T): GEMV kernel for small N, GEMM for prefill."""
+    N = n if n is not None else x2.shape[0]
+    if N < GEMM_MIN_BATCH_NB and not isinstance(lin, DenseLinear):
+        lin.gemv_into(x2, y, mode=mode, n=n, x_ld=x_ld)
+        return y
+    if x_ld:
+        x2 = torch.as_strided(x2, (N, lin.in_features), (x_ld, 1))
+    out = lin(x2.contiguous()) if not isinstance(lin, DenseLinear) \
+        else lin(x2)
+    if mode == _lib.EPI_STORE:
+        y.copy_(out)
+    elif mode == _lib.EPI_ADD:
+        y.add_(out)
+    elif mode == _lib.EPI_RELU2:
+        y.copy_(torch.relu(out))
+        y.mul_(y)
+    else:
+        raise NotImplementedError(mode)
+    return y
+
+
+class QuantRWKV7:
+    def __init__(self, ckpt, device="cuda"):
+        _lib.load()
+        self.device = torch.device(device)
+        self.naming = ckpt.naming
+        self.n_layer = ckpt.n_layer
+        self.n_embd = ckpt.n_embd
+        self.head_size = ckpt.head_size
+        self.n_head = ckpt.n_embd // ckpt.head_size
+        self.vocab_size = ckpt.vocab_size
+        if self.head_size != 64:
+            raise NotImplementedError("HIP WKV kernels are built for head 64")
+        t = ckpt.tensors
+        dev = self.device
+        self.emb = EmbTable(t["emb.weight"], dev)
+        self.head = make_linear(t["head.weight"], dev)
+        vec = lambda k: dense_param(t[k], dev).reshape(-1).contiguous()
+        if self.naming == "custom":
+            self.ln0_w, self.ln0_b = vec("ln0.weight"), vec("ln0.bias")
+        else:
+            self.ln0_w, self.ln0_b = vec("blocks.0.ln0.weight"), \
+                vec("blocks.0.ln0.bias")
+        self.ln_out_w, self.ln_out_b = vec("ln_out.weight"), vec("ln_out.bias")
+        self.blocks = [QuantBlock(t, f"blocks.{i}.", self.naming, i,
+                                  self.n_head, self.head_size, dev)
+                       for i in range(self.n_layer)]
+        b0 = self.blocks[-1]
+        self.ffn = b0.cmix.key.out_features
+        self.ranks = {b: A.shape[0] for b, (A, _) in
+                      self.blocks[-1].tmix.lora.items()}
+        self._work = {}
+        self._graphs = {}
+        torch.cuda.synchronize(dev)
+
+    # ------------------------------------------------------------ state
+    def init_state(self, batch_size=1):
+        H, S = self.n_head, self.head_size
+        return [(torch.zeros(batch_size, H, S, S, device=self.device), None,
+                 None) for _ in range(self.n_layer)]
+
+    def _work_for(self, N):
+        if N not in self._work:
+            self._work[N] = _Work(N, self.n_embd, self.ffn, self.ranks,
+                                  self.device)
+        return self._work[N]
+
+    # ---------------------------------------------------------- forward
+    def _idx(self, idx):
+        idx = torch.as_tensor(idx)
+        if idx.dim() == 1:
+            idx = idx[None]
+        if not idx.is_cuda:
+            if idx.numel() and (int(idx.min()) < 0
+                                or int(idx.max()) >= self.vocab_size):
+                raise ValueError("token id out of range")
+        return idx.to(device=self.device, dtype=torch.int64)
+
+    def _body(self, idx, states, wk, out_states):
+        """All layers for idx [B, T] (device int64); writes the new state
+        tensors into out_states (preallocated) and leaves ln_out(x) in
+        wk.xo."""
+        B, T = idx.shape
+        N, C, H = B * T, self.n_embd, self.n_head
+        st = _stream()
+        x = wk.x
+        self.emb.gather_into(idx.reshape(-1), x)
+        _lib.call("rwkvq_layer_norm", _lib.ptr(x), _lib.ptr(self.ln0_w),
+                  _lib.ptr(self.ln0_b), _lib.ptr(x), N, C, 1e-5, st)
+        for li, (blk, state) in enumerate(zip(self.blocks, states)):
+            tm, cm = blk.tmix, blk.cmix
+            wkv_in, tshift, cshift = state
+            wkv_out, tshift_out, cshift_out = out_states[li]
+            _lib.call("rwkvq_shift_lerp", _lib.ptr(x), _lib.ptr(blk.ln1_w),
+                      _lib.ptr(blk.ln1_b), _lib.ptr(tshift),
+                      _lib.ptr(tm.coef), 6, _lib.ptr(wk.xs),
+                      _lib.ptr(tshift_out), B, T, C, st)
+            if FUSE and tm.rkv_fused is not None and N < GEMM_MIN_BATCH_NB:
+                tm.rkv_fused.gemv_into(wk.xs, wk.rkv, N, 6 * C)
+            else:
+                xs_flat = wk.xs.view(N, 6 * C)
+                rkv_flat = wk.rkv.view(N, 3 * C)
+                for j, lin in enumerate((tm.r_proj, tm.k_proj, tm.v_proj)):
+                    yv = rkv_flat[:, j * C:(j + 1) * C]
+                    if N < GEMM_MIN_BATCH_NB:
+                        tmp = torch.empty(N, C, device=self.device)
+                        _apply(lin, xs_flat[:, j * C:], tmp, _lib.EPI_STORE,
+                               n=N, x_ld=6 * C)
+                    else:
+                        tmp = lin(wk.xs[:, j].contiguous())
+                    yv.copy_(tmp)
+            tm.run_lora(wk)
+            layer0 = 1 if li == 0 else 0
+            _lib.call("rwkvq_wkv_prep", _lib.ptr(wk.rkv),
+                      _lib.ptr(wk.yl["w"]), _lib.ptr(wk.yl["a"]),
+                      None if layer0 else _lib.ptr(wk.yl["v"]),
+                      _lib.ptr(tm.w0), _lib.ptr(tm.a0), _lib.ptr(tm.v0),
+                      _lib.ptr(tm.k_k), _lib.ptr(tm.k_a),
+                      _lib.ptr(wk.v_first), layer0, _lib.ptr(wk.w),
+                      _lib.ptr(wk.kp), _lib.ptr(wk.vp), _lib.ptr(wk.aa),
+                      _lib.ptr(wk.bb), N, C, self.head_size, st)
+            _lib.call("rwkvq_wkv7_scan", _lib.ptr(wk.rkv), 3 * C,
+                      _lib.ptr(wk.w), _lib.ptr(wk.kp), _lib.ptr(wk.vp),
+                      _lib.ptr(wk.aa), _lib.ptr(wk.bb), C, _lib.ptr(wkv_in),
+                      _lib.ptr(wkv_out), _lib.ptr(wk.y), C, B, T, H,
+                      self.head_size, st)
+            _lib.call("rwkvq_wkv_tail", _lib.ptr(wk.y), _lib.ptr(wk.rkv),
+                      _lib.ptr(wk.kp), _lib.ptr(wk.vp), _lib.ptr(wk.yl["g"]),
+                      _lib.ptr(tm.r_k), _lib.ptr(tm.ln_x_w),
+                      _lib.ptr(tm.ln_x_b), _lib.ptr(wk.o), N, C,
+                      self.head_size, st)
+            _apply(tm.o_proj, wk.o, x, _lib.EPI_ADD)
+            _lib.call("rwkvq_shift_lerp", _lib.ptr(x), _lib.ptr(blk.ln2_w),
+                      _lib.ptr(blk.ln2_b), _lib.ptr(cshift),
+                      _lib.ptr(cm.x_k), 1, _lib.ptr(wk.xk),
+                      _lib.ptr(cshift_out), B, T, C, st)
+            _apply(cm.key, wk.xk, wk.hk, _lib.EPI_RELU2)
+            _apply(cm.value, wk.hk, x, _lib.EPI_ADD)
+        _lib.call("rwkvq_layer_norm", _lib.ptr(x), _lib.ptr(self.ln_out_w),
+                  _lib.ptr(self.ln_out_b), _lib.ptr(wk.xo), N, C, 1e-5, st)
+
+    def _new_states(self, B):
+        H, S, C = self.n_head, self.head_size, self.n_embd
+        dev = self.device
+        return [(torch.empty(B, H, S, S, device=dev),
+                 torch.empty(B, 1, C, device=dev),
+                 torch.empty(B, 1, C, device=dev))
+                for _ in range(self.n_layer)]
+
+    def forward_hidden(self, idx, states):
+        """Hidden state after ln_out, before the head: [B, T, D]."""
+        idx = self._idx(idx)
+        B, T = idx.shape
+        wk = self._work_for(B * T)
+        out = self._new_states(B)
+        self._body(idx, states, wk, out)
+        return wk.xo.reshape(B, T, -1).clone(), out
+
+    def forward_stateful(self, idx, states, last_only=False, tail_only=0):
+        """idx [B, T] -> (logits [B, T', V], new_states)."""
+        idx = self._idx(idx)
+        B, T = idx.shape
+        wk = self._work_for(B * T)
+        out = self._new_states(B)
+        self._body(idx, states, wk, out)
+        xo = wk.xo.reshape(B, T, -1)
+        if last_only and T > 1:
+            xo = xo[:, -1:]
+        elif tail_only and T > tail_only:
+            xo = xo[:, -tail_only:]
+        xo = xo.reshape(-1, self.n_embd).contiguous()
+        logits = torch.empty(xo.shape[0], self.vocab_size, device=self.device)
+        _apply(self.head, xo, logits, _lib.EPI_STORE)
+        return logits.reshape(B, -1, self.vocab_size), out
+
+    def __call__(self, idx):
+        idx = self._idx(idx)
+        return self.forward_stateful(idx, self.init_state(idx.shape[0]))[0]
+
+    # ------------------------------------------------- graph-replay decode
+    def step(self, idx, states):
+        """Decode step (T = 1 per sequence).  With USE_GRAPH the whole step
+        is captured once per batch size into a HIP graph with static
+        buffers and replayed; states are copied into / out of the graph's
+        buffers (device-to-device)."""
+        idx = self._idx(idx)
+        B, T = idx.shape
+        if not USE_GRAPH or T != 1:
+            return self.forward_stateful(idx, states)
+        g = self._graphs.get(B)
+        if g is None:
+            g = self._capture(B)
+            self._graphs[B] = g
+        g["idx"].copy_(idx)
+        for (si, ti, ci), (wi, tsi, csi) in zip(g["in"], states):
+            si.copy_(wi)
+            if tsi is None:
+                ti.zero_()
+            else:
+                ti.copy_(tsi)
+            if csi is None:
+                ci.zero_()
+            else:
+                ci.copy_(csi)
+        g["graph"].replay()
+        new = [(s.clone(), t.clone(), c.clone()) for s, t, c in g["out"]]
+        return g["logits"].clone().reshape(B, 1, -1), new
+
+    def _capture(self, B):
+        dev = self.device
+        idx = torch.zeros(B, 1, dtype=torch.int64, device=dev)
+        st_in = self._new_states(B)
+        for s in st_in:
+            for t in s:
+                t.zero_()
+        st_out = self._new_states(B)
+        wk = self._work_for(B)
+        logits = torch.empty(B, self.vocab_size, device=dev)
+
+        def run():
+            self._body(idx, st_in, wk, st_out)
+            _apply(self.head, wk.xo, logits, _lib.EPI_STORE)
+
+        s = torch.cuda.Stream(device=dev)
+        s.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(s):
+            run()                       # warm-up outside the graph
+        torch.cuda.current_stream(dev).wait_stream(s)
+        torch.cuda.synchronize(dev)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            run()
+        torch.cuda.synchronize(dev)
+        return {"graph": graph, "idx": idx, "in": st_in, "out": st_out,
+                "logits": logits}
+
+    def decode_replay(self, B):
+        """Replay the captured decode graph for batch B on its static
+        buffers (benchmark hook: no state copies)."""
+        g = self._graphs.get(B)
+        if g is None:
+            g = self._capture(B)
+            self._graphs[B] = g
+        g["graph"].replay()
+        return g

@@ -112,5 +112,5 @@ def test_shape_errors_raise():
     lin = GwQuantLinear(qt_for("sb6", 4, _w(64, 512, seed=1)))
     with pytest.raises(_lib.HipKernelError):
         _lib.call("rwkvq_gemv_sb6", _lib.ptr(lin.nib), None,
-                  _lib.ptr(lin.rec), 4, 64, 500, 64, None, None, 1, 0,
+                  _lib.ptr(lin.rec), 4, 64, 500, 64, None, 0, None, 1, 0,
                   _lib.stream_handle())
