@@ -107,32 +107,14 @@ def cpu_baseline(qts, budget_s=15.0):
                       f"numpy dequant to fp32 + fp32 GEMV, {t_total:.1f} s"}
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--copies", type=int, default=4)
-    ap.add_argument("--no-cpu", action="store_true")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU only (asked for "
-              f"--gpus {args.gpus}); run with --gpus 1", file=sys.stderr)
-        sys.exit(2)
-
+def gemv_set_bench(args, qts, dev):
+    """Time the 3-GEMV set on rotating device copies, replayed from a HIP
+    graph (launch gaps as a serving loop sees them)."""
     import torch
-    from rwkv_quant.backends.hip import _lib
     from rwkv_quant.backends.hip.quant_linear import (QuantLinearV2,
                                                       SymQuantLinear)
-    _lib.load()
-    qts = build_set()
-    per = algorithmic_bytes(qts)
-    set_bytes = sum(per.values())
-    dev = torch.device("cuda:0")
-
     base = {n: (QuantLinearV2(qt) if n == "head" else SymQuantLinear(qt))
             for n, qt in qts.items()}
-    # distinct device copies of every buffer
     copies = []
     for c in range(args.copies):
         cp = {}
@@ -150,47 +132,136 @@ def main():
          .float().to(dev) for n, qt in qts.items()}
     y = {n: torch.empty(1, qt.shape[0], device=dev) for n, qt in qts.items()}
 
-    def step(i):
-        cp = copies[i % len(copies)]
-        for n in SHAPES:
-            cp[n].gemv_into(x[n], y[n])
+    def one_pass(names=SHAPES):
+        for cp in copies:
+            for n in names:
+                cp[n].gemv_into(x[n], y[n])
 
-    for i in range(args.warmup):
-        step(i)
+    def graph_of(names=SHAPES):
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            one_pass(names)
+        torch.cuda.current_stream(dev).wait_stream(side)
+        torch.cuda.synchronize()
+        gph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gph):
+            one_pass(names)
+        return gph
+
+    set_graph = graph_of()
+    reps = max(1, args.steps // args.copies)
+    for _ in range(max(1, args.warmup // args.copies)):
+        set_graph.replay()
     torch.cuda.synchronize()
-
     stream = torch.cuda.current_stream()
-    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(
-        enable_timing=True)
-    torch.cuda.synchronize()
+    t0, t1 = (torch.cuda.Event(enable_timing=True) for _ in range(2))
     t0.record(stream)
-    for i in range(args.steps):
-        step(i)
+    for _ in range(reps):
+        set_graph.replay()
     t1.record(stream)
     torch.cuda.synchronize()
-    ms_per_step = t0.elapsed_time(t1) / args.steps
+    steps = reps * args.copies
+    ms_per_step = t0.elapsed_time(t1) / steps
 
-    # per-kernel mean launch time (events on the launch stream)
+    # mean launch time of each kernel on its own (graph of that kernel only)
     kern = {}
     for n in SHAPES:
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(
-            enable_timing=True)
-        reps = args.steps
+        gk = graph_of((n,))
+        gk.replay()
         torch.cuda.synchronize()
+        e0, e1 = (torch.cuda.Event(enable_timing=True) for _ in range(2))
         e0.record(stream)
-        for i in range(reps):
-            copies[i % len(copies)][n].gemv_into(x[n], y[n])
+        for _ in range(reps):
+            gk.replay()
         e1.record(stream)
         torch.cuda.synchronize()
-        kern[n] = e0.elapsed_time(e1) / reps
-    head_us = kern["head"] * 1e3
+        kern[n] = e0.elapsed_time(e1) / (reps * args.copies)
+    return ms_per_step, steps, kern
+
+
+def decode_bench(preset, batches, n_tok, dev):
+    """ms per decode step of the 1.5B-shaped model (graph replay, state
+    carried between steps, fresh uniform-random token ids each step)."""
+    import torch
+    from rwkv_quant.backends.hip.quant_model import QuantRWKV7
+    from rwkv_quant.models.synthetic import SHAPES as MS, quantized_model
+    t0 = time.time()
+    ck = quantized_model(preset, seed=0, device=dev, **{
+        k: v for k, v in MS["1.5b"].items() if k != "vocab"},
+        vocab=MS["1.5b"]["vocab"])
+    model = QuantRWKV7(ck, device=dev)
+    del ck
+    build_s = time.time() - t0
+    out = {"build_s": round(build_s, 1)}
+    g = torch.Generator(device=dev).manual_seed(2)
+    for B in batches:
+        ids = torch.randint(0, 65536, (n_tok, B), generator=g, device=dev)
+        for t in range(4):                     # warm-up + capture
+            model.decode_replay(B, ids[t])
+        model.reset_replay_state(B)
+        torch.cuda.synchronize()
+        e0, e1 = (torch.cuda.Event(enable_timing=True) for _ in range(2))
+        e0.record()
+        for t in range(n_tok):
+            model.decode_replay(B, ids[t])
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / n_tok
+        out[f"b{B}_ms_per_step"] = round(ms, 4)
+        out[f"b{B}_tok_s"] = round(B * 1e3 / ms, 1)
+    return model, out
+
+
+def prefill_bench(model, T, dev, reps=3):
+    import torch
+    g = torch.Generator(device=dev).manual_seed(3)
+    idx = torch.randint(0, 65536, (1, T), generator=g, device=dev)
+    st = model.init_state(1)
+    model.forward_stateful(idx, st)              # warm-up
+    torch.cuda.synchronize()
+    e0, e1 = (torch.cuda.Event(enable_timing=True) for _ in range(2))
+    e0.record()
+    for _ in range(reps):
+        model.forward_stateful(idx, st)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    return {"T": T, "ms": round(ms, 3), "tok_s": round(T * 1e3 / ms, 1)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--copies", type=int, default=4)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-model", action="store_true",
+                    help="skip the 1.5B decode / pp512 measurements")
+    ap.add_argument("--decode-tokens", type=int, default=128)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for "
+              f"--gpus {args.gpus}); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from rwkv_quant.backends.hip import _lib
+    _lib.load()
+    dev = torch.device("cuda:0")
+    qts = build_set()
+    per = algorithmic_bytes(qts)
+    set_bytes = sum(per.values())
+    ms_per_step, steps, kern = gemv_set_bench(args, qts, dev)
     achieved = per["head"] / (kern["head"] * 1e-3) / 1e9
+    value = set_bytes / (ms_per_step * 1e-3) / 1e9
 
     out = {
         "metric": "quant GEMV GB/s (% HBM peak)",
-        "value": round(set_bytes / (ms_per_step * 1e-3) / 1e9, 2),
+        "value": round(value, 2),
         "unit": "GB/s",
-        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "n_gpus": 1, "steps": steps, "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 5),
         "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None,
@@ -199,18 +270,33 @@ def main():
                 "columns, bf16 N(0,1) x)",
         "config": {"workload": "configs[1]: sym@6 cmix key 2048->8192 + "
                                "value 8192->2048 + rtn@8 head 2048->65536, "
-                               "batch 1",
+                               "batch 1, HIP-graph replay over 4 device "
+                               "copies (650 MB)",
                    "set_bytes": set_bytes, "copies": args.copies},
-        "pct_hbm_peak": round(100 * set_bytes / (ms_per_step * 1e-3) / 1e9
-                              / HBM_PEAK_GBS, 2),
+        "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "kernels_us": {n: round(v * 1e3, 3) for n, v in kern.items()},
         "roofline": {"bound": "hbm", "kernel": "gemv_kernel<F_RTN8> (head)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None, "launch_us": round(head_us, 3),
+                     "traffic": None,
+                     "launch_us": round(kern["head"] * 1e3, 3),
                      "bytes_per_launch": per["head"]},
         "cpu_baseline": None,
     }
+    if not args.no_model:
+        model, dec = decode_bench("compression", (1, 8), args.decode_tokens,
+                                  dev)
+        out["decode_1p5b_compression"] = dec
+        del model
+        torch.cuda.empty_cache()
+        model, dec_r = decode_bench("reduction", (1,), 32, dev)
+        out["decode_1p5b_reduction"] = dec_r
+        pf = prefill_bench(model, 512, dev)
+        flop = 2 * 1_392_246_784 * 512
+        pf["tflop_s"] = round(flop / (pf["ms"] * 1e-3) / 1e12, 2)
+        out["pp512_1p5b_reduction"] = pf
+        del model
+        torch.cuda.empty_cache()
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(qts)
     print(json.dumps(out), flush=True)

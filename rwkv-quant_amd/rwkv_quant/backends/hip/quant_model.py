@@ -466,6 +466,7 @@ class QuantRWKV7:
             g = self._capture(B)
             self._graphs[B] = g
         g["idx"].copy_(idx)
+        g["next"] = 0
         for (si, ti, ci), (wi, tsi, csi) in zip(g["in"], states):
             si.copy_(wi)
             if tsi is None:
@@ -481,39 +482,65 @@ class QuantRWKV7:
         return g["logits"].clone().reshape(B, 1, -1), new
 
     def _capture(self, B):
+        """Two graphs of one decode step over static buffers: graph 0 reads
+        state set 0 and writes set 1, graph 1 the reverse, so a replayed
+        token stream carries its state without copies."""
         dev = self.device
         idx = torch.zeros(B, 1, dtype=torch.int64, device=dev)
-        st_in = self._new_states(B)
-        for s in st_in:
-            for t in s:
-                t.zero_()
-        st_out = self._new_states(B)
+        sets = [self._new_states(B), self._new_states(B)]
+        for st in sets:
+            for s in st:
+                for t in s:
+                    t.zero_()
         wk = self._work_for(B)
         logits = torch.empty(B, self.vocab_size, device=dev)
 
-        def run():
-            self._body(idx, st_in, wk, st_out)
+        def run(src, dst):
+            self._body(idx, src, wk, dst)
             _apply(self.head, wk.xo, logits, _lib.EPI_STORE)
 
-        s = torch.cuda.Stream(device=dev)
-        s.wait_stream(torch.cuda.current_stream(dev))
-        with torch.cuda.stream(s):
-            run()                       # warm-up outside the graph
-        torch.cuda.current_stream(dev).wait_stream(s)
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            run(sets[0], sets[1])           # warm-up outside the graph
+        torch.cuda.current_stream(dev).wait_stream(side)
         torch.cuda.synchronize(dev)
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            run()
+        graphs = []
+        for k in range(2):
+            gph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gph):
+                run(sets[k], sets[1 - k])
+            graphs.append(gph)
         torch.cuda.synchronize(dev)
-        return {"graph": graph, "idx": idx, "in": st_in, "out": st_out,
-                "logits": logits}
+        for st in sets:
+            for s in st:
+                for t in s:
+                    t.zero_()
+        return {"graphs": graphs, "idx": idx, "sets": sets, "logits": logits,
+                "next": 0, "in": sets[0], "out": sets[1],
+                "graph": graphs[0]}
 
-    def decode_replay(self, B):
-        """Replay the captured decode graph for batch B on its static
-        buffers (benchmark hook: no state copies)."""
+    def decode_replay(self, B, ids=None):
+        """Benchmark/serving hook: one decode step of batch B on the
+        captured graphs, carrying the state in the static buffers
+        (ping-pong).  `ids` (device int64 [B]) is copied into the input
+        slot first.  Returns the static logits buffer [B, V]."""
         g = self._graphs.get(B)
         if g is None:
             g = self._capture(B)
             self._graphs[B] = g
-        g["graph"].replay()
-        return g
+        if ids is not None:
+            g["idx"].copy_(ids.reshape(B, 1))
+        g["graphs"][g["next"]].replay()
+        g["next"] ^= 1
+        return g["logits"]
+
+    def reset_replay_state(self, B):
+        g = self._graphs.get(B)
+        if g is None:
+            return
+        for st in g["sets"]:
+            for s in st:
+                for t in s:
+                    t.zero_()
+        g["next"] = 0

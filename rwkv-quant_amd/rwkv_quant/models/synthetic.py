@@ -30,21 +30,24 @@ def lora_ranks(d):
 
 
 def world_state_dict(n_layer, n_embd, head_size=64, vocab=65536, ffn=None,
-                     seed=0, std=0.02, dtype=torch.bfloat16):
-    """Random-init state dict with world naming (LoRA stored [in, out])."""
-    g = torch.Generator().manual_seed(seed)
+                     seed=0, std=0.02, dtype=torch.bfloat16, device="cpu"):
+    """Random-init state dict with world naming (LoRA stored [in, out]).
+    `device` selects where the tensors are drawn (a GPU generator gives a
+    different, equally seeded stream)."""
+    g = torch.Generator(device=device).manual_seed(seed)
     C, H, N = n_embd, n_embd // head_size, head_size
     ffn = ffn or 4 * C
     r = lora_ranks(C)
 
     def rn(*shape, s=std):
-        return (torch.randn(*shape, generator=g) * s).to(dtype)
+        return (torch.randn(*shape, generator=g, device=device) * s).to(dtype)
 
     def uni(*shape, lo=0.0, hi=1.0):
-        return (lo + (hi - lo) * torch.rand(*shape, generator=g)).to(dtype)
+        return (lo + (hi - lo) * torch.rand(*shape, generator=g,
+                                            device=device)).to(dtype)
 
-    one = lambda *s: torch.ones(*s, dtype=dtype)
-    zero = lambda *s: torch.zeros(*s, dtype=dtype)
+    one = lambda *s: torch.ones(*s, dtype=dtype, device=device)
+    zero = lambda *s: torch.zeros(*s, dtype=dtype, device=device)
     sd = {"emb.weight": rn(vocab, C)}
     for i in range(n_layer):
         p = f"blocks.{i}."
@@ -56,8 +59,8 @@ def world_state_dict(n_layer, n_embd, head_size=64, vocab=65536, ffn=None,
         for nm in ("x_r", "x_w", "x_k", "x_v", "x_a", "x_g"):
             sd[a + nm] = uni(1, 1, C)
         sd[a + "w1"], sd[a + "w2"] = rn(C, r["w"]), rn(r["w"], C)
-        sd[a + "w0"] = (torch.randn(1, 1, C, generator=g) * 0.5 - 0.5) \
-            .to(dtype)
+        sd[a + "w0"] = (torch.randn(1, 1, C, generator=g, device=device) * 0.5
+                        - 0.5).to(dtype)
         sd[a + "a1"], sd[a + "a2"] = rn(C, r["a"]), rn(r["a"], C)
         sd[a + "a0"] = rn(1, 1, C, s=0.5)
         if i > 0:
@@ -80,12 +83,15 @@ def world_state_dict(n_layer, n_embd, head_size=64, vocab=65536, ffn=None,
 
 
 def quantized_model(preset, n_layer, n_embd, head_size=64, vocab=65536,
-                    ffn=None, seed=0, config=None):
-    """Random-init model quantized with a preset -> QuantizedCheckpoint."""
+                    ffn=None, seed=0, config=None, device="cpu"):
+    """Random-init model quantized with a preset -> QuantizedCheckpoint.
+    With a GPU `device` the weights are drawn and quantized there (the
+    quantizer is plain torch) and only the packed fields come back."""
     from ..formats import writer
     from ..presets import PRESETS
     cfg = config if config is not None else PRESETS[preset]
-    sd = world_state_dict(n_layer, n_embd, head_size, vocab, ffn, seed)
+    sd = world_state_dict(n_layer, n_embd, head_size, vocab, ffn, seed,
+                          device=device)
     ck = writer.quantize_state_dict(sd, cfg, naming="world", n_layer=n_layer,
                                     n_embd=n_embd, head_size=head_size,
                                     vocab_size=vocab)
