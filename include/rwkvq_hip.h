@@ -55,7 +55,7 @@ extern "C" {
  * (x_ld = 0 means packed: (rows / out_per) * IN); y is fp32 [n_cols, rows].
  * out_per == rows is the plain GEMV; out_per < rows runs K = rows/out_per
  * row-concatenated matrices with their own inputs in one launch (the fused
- * r/k/v projection).  IN % 256 == 0, IN <= 8192, out_per % 2 == 0.
+ * r/k/v projection).  IN % 256 == 0, IN <= 16384, out_per % 2 == 0.
  * Inputs are rounded to fp16 pairs; products and sums are fp32.
  *
  * Replaces:
@@ -128,7 +128,8 @@ int rwkvq_layer_norm(const float* x, const float* w, const float* b, float* y,
 /* LN (eps 1e-5) + token shift + ncoef lerps for x [B, T, D]:
  * out[(b*T+t), c, :] = xn + (shift - xn) * coef[c, :], shift = xn of the
  * previous token or prev[b] (zeros if prev is NULL) at t = 0;
- * new_prev[b] = xn of the last token (may be NULL).
+ * new_prev[b] = xn of the last token (may be NULL).  ncoef is 1 or 6;
+ * D <= 4096.
  * Replaces: _token_shift_stateful + the six lerps of the time mix and the
  * one of the channel mix (reference: quant_model.py:292-301, 643-650,
  * 803-809). */
@@ -173,9 +174,22 @@ int rwkvq_wkv_tail(const float* y, const float* rkv, const float* kp,
                    const float* ln_w, const float* ln_b, float* out, int N,
                    int D, int head_size, void* stream);
 
+/* Decode (T = 1) time-mix core in one launch per (sequence, head):
+ * rwkvq_wkv_prep + one rwkvq_wkv7_scan step + rwkvq_wkv_tail for
+ * rkv [B, 3, D] and LoRA outputs [B, D]; state_in -> state_out (may alias).
+ * Replaces: the decode path of _forward_stateful_fused from the LoRA
+ * outputs to the o_proj input (reference: quant_model.py:693-720). */
+int rwkvq_wkv7_decode(const float* rkv, const float* yw, const float* ya,
+                      const float* yv, const float* g, const float* w0,
+                      const float* a0, const float* v0, const float* k_k,
+                      const float* k_a, const float* r_k, const float* ln_w,
+                      const float* ln_b, float* v_first, int layer0,
+                      const float* state_in, float* state_out, float* out,
+                      int B, int H, int head_size, void* stream);
+
 /* Grouped dense-fp16 GEMV of up to 4 low-rank branches in one launch:
  * y_j[n, r] = epi_j( sum_c x_j[n * x_ld_j + c] * W_j[r, c] ), n < N <= 8.
- * in_j % 16 == 0 (and % 128 when in_j > 512).
+ * in_j % 16 == 0 and in_j <= 512, or in_j in {2048, 2560}.
  * Replaces: QuantTMix._lora down/up products (reference:
  * quant_model.py:462-526). */
 int rwkvq_lora_gemv(int n_jobs, const void* const* W, const float* const* x,

@@ -129,8 +129,44 @@ __device__ __forceinline__ void decode_raw(const Raw& r, uint32_t h[16]) {
   }
 }
 
+// Convert one lane's 32 x values of group g into the format's 16 fp16
+// pairs and the three block sums (A, B halves in fp16-rounded values, and
+// the fp32 sum used by the sb6 min term).
+template <int FMT>
+__device__ __forceinline__ void x_group(const float* __restrict__ xp,
+                                        uint32_t* __restrict__ dst,
+                                        float* __restrict__ sums) {
+  float xv[32];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    float4 f = reinterpret_cast<const float4*>(xp)[t];
+    xv[4 * t] = f.x; xv[4 * t + 1] = f.y; xv[4 * t + 2] = f.z;
+    xv[4 * t + 3] = f.w;
+  }
+  float sa = 0.f, sb = 0.f, sf = 0.f;
+  uint32_t pk[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    int c0, c1;
+    x_cols<FMT>(i, c0, c1);
+    pk[i] = pack_h2(xv[c0], xv[c1]);
+    const float s2 = h2_lo(pk[i]) + h2_hi(pk[i]);
+    if (i < 8) sa += s2; else sb += s2;
+  }
+#pragma unroll
+  for (int c = 0; c < 32; ++c) sf += xv[c];
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    reinterpret_cast<uint4*>(dst)[q] =
+        make_uint4(pk[4 * q], pk[4 * q + 1], pk[4 * q + 2], pk[4 * q + 3]);
+  const float mb = magic_bias<FMT>();
+  sums[0] = -mb * sa;
+  sums[1] = -mb * sb;
+  sums[2] = sf;
+}
+
 template <int FMT, int NN, int RS>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(512)
 gemv_kernel(GemvArgs a) {
   const int lane = threadIdx.x & 63;
   // wave-uniform values live in SGPRs: row addressing becomes scalar and
@@ -142,15 +178,21 @@ gemv_kernel(GemvArgs a) {
   const int g = kslice * 64 + lane;
   const bool active = g < ng;
   const int gl = active ? g : 0;               // in-bounds group for loads
-  const int row_base = (blockIdx.x * a.rg + rgi) * a.rpw;
+  const int wg_row0 = blockIdx.x * a.rg * a.rpw;
+  const int row_base = wg_row0 + rgi * a.rpw;
   const int nsb = a.in >> 8;
 
-  __shared__ float red[4 * RS * NN];
+  // x of this workgroup's segment, staged once per workgroup as fp16 pairs
+  // [NN][ng][16] followed by the sums [NN][ng][3] (dynamic LDS)
+  extern __shared__ uint32_t smem[];
+  uint32_t* s_xh = smem;
+  float* s_xs = reinterpret_cast<float*>(smem + NN * ng * 16);
+  __shared__ float red[8 * RS * NN];
 
-  // first weight batch in flight before x is fetched: the two HBM round
-  // trips overlap instead of adding up.  Loads are unconditional (row index
-  // clamped into the matrix) so the compiler can count them and wait only
-  // for the batch it consumes.
+  // first weight batch in flight before x is fetched: the two memory round
+  // trips overlap.  Loads are unconditional (row index clamped into the
+  // matrix) so the compiler can count them and wait only for the batch it
+  // consumes.
   const int nrows = min(a.rpw, a.rows - row_base);   // rows of this wave
   const int last = a.rows - 1;
   Raw cur[RS], nxt[RS];
@@ -158,40 +200,34 @@ gemv_kernel(GemvArgs a) {
   for (int j = 0; j < RS; ++j)
     load_raw<FMT>(a, min(row_base + j, last), ng, nsb, gl, cur[j]);
 
-  // ---- lane-resident x: 16 fp16 pairs per column + block sums
-  const int seg = row_base < a.rows ? row_base / a.out_per : 0;
+  const int seg = wg_row0 < a.rows ? wg_row0 / a.out_per : 0;
+  for (int item = threadIdx.x; item < NN * ng; item += blockDim.x) {
+    const int n = item / ng, gg = item % ng;
+    if (n < a.n) {
+      x_group<FMT>(a.x + (size_t)n * a.x_ld + (size_t)seg * a.in +
+                       (size_t)gg * 32,
+                   s_xh + (size_t)item * 16, s_xs + (size_t)item * 3);
+    } else {
+#pragma unroll
+      for (int q = 0; q < 16; ++q) s_xh[(size_t)item * 16 + q] = 0u;
+      s_xs[item * 3] = s_xs[item * 3 + 1] = s_xs[item * 3 + 2] = 0.f;
+    }
+  }
+  __syncthreads();
   uint32_t xh[NN][16];
   float xsa[NN], xsb[NN], xsf[NN];
 #pragma unroll
   for (int n = 0; n < NN; ++n) {
-    float sa = 0.f, sb = 0.f, sf = 0.f;
-    if (active && n < a.n) {
-      const float* xp =
-          a.x + (size_t)n * a.x_ld + (size_t)seg * a.in + (size_t)g * 32;
-      float xv[32];
+    const uint4* src = reinterpret_cast<const uint4*>(s_xh + (n * ng + gl) * 16);
 #pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        float4 f = reinterpret_cast<const float4*>(xp)[t];
-        xv[4 * t] = f.x; xv[4 * t + 1] = f.y;
-        xv[4 * t + 2] = f.z; xv[4 * t + 3] = f.w;
-      }
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        int c0, c1;
-        x_cols<FMT>(i, c0, c1);
-        uint32_t p = pack_h2(xv[c0], xv[c1]);
-        xh[n][i] = p;
-        float s2 = h2_lo(p) + h2_hi(p);
-        if (i < 8) sa += s2; else sb += s2;
-      }
-#pragma unroll
-      for (int c = 0; c < 32; ++c) sf += xv[c];
-    } else {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) xh[n][i] = 0u;
+    for (int q = 0; q < 4; ++q) {
+      uint4 v = src[q];
+      xh[n][4 * q] = v.x; xh[n][4 * q + 1] = v.y;
+      xh[n][4 * q + 2] = v.z; xh[n][4 * q + 3] = v.w;
     }
-    const float mb = magic_bias<FMT>();
-    xsa[n] = -mb * sa; xsb[n] = -mb * sb; xsf[n] = sf;
+    xsa[n] = s_xs[(n * ng + gl) * 3];
+    xsb[n] = s_xs[(n * ng + gl) * 3 + 1];
+    xsf[n] = s_xs[(n * ng + gl) * 3 + 2];
   }
 
   // per-lane constants for sb6 scale extraction (block k of its superblock)
@@ -310,28 +346,41 @@ gemv_kernel(GemvArgs a) {
 
 template <int FMT, int RS>
 int launch_rs(GemvArgs a, hipStream_t s) {
-  // rows per wave: aim for RWKVQ_TARGET_WAVES waves, at least RS rows; a
-  // wave's rows share one x segment
+  // rows per wave: aim for RWKVQ_TARGET_WAVES waves, at least RS rows; the
+  // rows of a workgroup share one x segment (out_per multiple of them)
   long rows_waves = (long)a.rows * a.ks;
   int rpw = (int)(rows_waves / RWKVQ_TARGET_WAVES);
   rpw = rpw < RS ? RS : (rpw / RS) * RS;
   if (rpw > RWKVQ_MAX_RPW) rpw = RWKVQ_MAX_RPW;
-  while (rpw > RS && a.out_per % rpw) rpw -= RS;
-  if (a.out_per % rpw) return RWKVQ_ERR_ARG;
+  while (a.rg > 1 && a.out_per % (a.rg * RS)) a.rg >>= 1;
+  while (rpw > RS && a.out_per % (a.rg * rpw)) rpw -= RS;
+  if (a.out_per % (a.rg * rpw)) return RWKVQ_ERR_ARG;
   a.rpw = rpw;
   const int rows_per_wg = a.rg * rpw;
   dim3 grid((a.rows + rows_per_wg - 1) / rows_per_wg);
   dim3 block(64 * a.ks * a.rg);
-  for (int n0 = 0; n0 < a.n; n0 += 4) {
+  const int ng = a.in / 32;
+  // up to 8 input rows per launch (each weight read once per chunk); the
+  // staged x must fit the LDS budget of 96 KiB per workgroup
+  int chunk = 8;
+  while (chunk > 1 && (size_t)chunk * ng * (16 + 3) * 4 > 96 * 1024) chunk >>= 1;
+  for (int n0 = 0; n0 < a.n; n0 += chunk) {
     GemvArgs b = a;
     b.x = a.x + (size_t)n0 * a.x_ld;
     b.y = a.y + (size_t)n0 * a.rows;
-    b.n = a.n - n0 < 4 ? a.n - n0 : 4;
-    switch (b.n) {
-      case 1: hipLaunchKernelGGL((gemv_kernel<FMT, 1, RS>), grid, block, 0, s, b); break;
-      case 2: hipLaunchKernelGGL((gemv_kernel<FMT, 2, RS>), grid, block, 0, s, b); break;
-      case 3: hipLaunchKernelGGL((gemv_kernel<FMT, 3, RS>), grid, block, 0, s, b); break;
-      default: hipLaunchKernelGGL((gemv_kernel<FMT, 4, RS>), grid, block, 0, s, b); break;
+    b.n = a.n - n0 < chunk ? a.n - n0 : chunk;
+    const int nn = b.n <= 1 ? 1 : b.n <= 2 ? 2 : b.n <= 4 ? 4 : 8;
+    const size_t lds = (size_t)nn * ng * (16 + 3) * 4;
+    switch (nn) {
+      case 1: hipLaunchKernelGGL((gemv_kernel<FMT, 1, RS>), grid, block, lds, s, b); break;
+      case 2: hipLaunchKernelGGL((gemv_kernel<FMT, 2, RS>), grid, block, lds, s, b); break;
+      case 4: hipLaunchKernelGGL((gemv_kernel<FMT, 4, RS>), grid, block, lds, s, b); break;
+      default:
+        if constexpr (RS == 2)   // 8 columns x 4 rows would spill VGPRs
+          hipLaunchKernelGGL((gemv_kernel<FMT, 8, RS>), grid, block, lds, s, b);
+        else
+          return RWKVQ_ERR_ARG;
+        break;
     }
   }
   return hipGetLastError() == hipSuccess ? RWKVQ_OK : RWKVQ_ERR_LAUNCH;
@@ -341,15 +390,12 @@ template <int FMT>
 int launch_fmt(GemvArgs a, hipStream_t s) {
   const int ng = a.in / 32;
   a.ks = (ng + 63) / 64;
-  if (a.ks > 4) return RWKVQ_ERR_SIZE;          // IN > 8192 not tiled here
-  a.rg = 4 / a.ks;
-  if (a.rg < 1) a.rg = 1;
+  if (a.ks > 8) return RWKVQ_ERR_SIZE;             // IN <= 16384
+  a.rg = a.ks >= 8 ? 1 : 8 / a.ks;  // <= 8 waves per workgroup share x
   // small matrices: 2-row batches keep more waves in flight; large ones
   // amortise the lane-resident x over 4-row batches
-  if ((long)a.rows * a.ks <= 8192 && a.out_per % 4 != 0)
+  if ((long)a.rows * a.ks <= 8192 || a.out_per % 4 || a.n > 4)
     return launch_rs<FMT, 2>(a, s);
-  if ((long)a.rows * a.ks <= 8192) return launch_rs<FMT, 2>(a, s);
-  if (a.out_per % 4) return launch_rs<FMT, 2>(a, s);
   return launch_rs<FMT, 4>(a, s);
 }
 

@@ -35,54 +35,132 @@ __device__ __forceinline__ float epi_apply(float v, int epi) {
   }
 }
 
-// One wave handles 8 rows; each row is split over 8 lanes (in <= 512) or the
-// wave walks one row at a time with 64 lanes (wide rows).  N <= 8 inputs.
+// One wave handles 8 rows of one branch.
+// Wide rows (in = 64 * PER, PER in {32, 40}): the 64 lanes split each row,
+// lane owns PER columns; 4 rows are decoded together so their weight loads
+// are in flight at once, x is read once per (wave, input row).
+// Narrow rows (in <= 512): 8 lanes per row, lane owns in/8 columns.
+// All column loops are fully unrolled (guards up to kMaxPer) so every load
+// of a row is issued before the first use.
+constexpr int kMaxPer = 64;
+
+template <int PER>
+__device__ __forceinline__ void lora_wide(const LoraJob& jo, int N, int lw, int lane) {
+  // lane l owns fp16 pairs p = l + 64 q (q < PER / 2): consecutive lanes
+  // read consecutive dwords of the row (coalesced 256 B per instruction)
+  constexpr int PW = PER / 2;
+  float res[2][8][4];                          // stores deferred to the end
+#pragma unroll
+  for (int r0 = 0; r0 < 8; r0 += 4) {
+    uint32_t wv[4][PW];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int row = min(lw * 8 + r0 + j, jo.rows - 1);
+      const uint32_t* wr =
+          reinterpret_cast<const uint32_t*>(jo.W + (size_t)row * jo.in);
+#pragma unroll
+      for (int q = 0; q < PW; ++q) wv[j][q] = wr[lane + 64 * q];
+    }
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+      if (n >= N) break;
+      const float2* xp =
+          reinterpret_cast<const float2*>(jo.x + (size_t)n * jo.x_ld);
+      uint32_t xh[PW];
+#pragma unroll
+      for (int q = 0; q < PW; ++q) {
+        const float2 f = xp[lane + 64 * q];
+        xh[q] = pack_h2(f.x, f.y);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float a = 0.f;
+#pragma unroll
+        for (int q = 0; q < PW; ++q) a = dot2(wv[j][q], xh[q], a);
+        res[r0 >> 2][n][j] = wave_sum_dpp(a);
+      }
+    }
+  }
+  if (lane < 8) {
+#pragma unroll
+    for (int rr = 0; rr < 8; ++rr) {
+      const int row = lw * 8 + rr;
+      if (rr != lane || row >= jo.rows) continue;
+#pragma unroll
+      for (int n = 0; n < 8; ++n)
+        if (n < N)
+          jo.y[(size_t)n * jo.y_ld + row] =
+              epi_apply(res[rr >> 2][n][rr & 3], jo.epi);
+    }
+  }
+}
+
+__device__ __forceinline__ void lora_narrow(const LoraJob& jo, int N, int lw, int lane) {
+  // 8 lanes per row; lane sub owns fp16 pairs p = sub + 8 q
+  const int sub = lane & 7, row = lw * 8 + (lane >> 3);
+  const int pairs = jo.in >> 1;
+  const bool live = row < jo.rows;
+  const uint32_t* wr = reinterpret_cast<const uint32_t*>(
+      jo.W + (size_t)(live ? row : 0) * jo.in);
+  uint32_t wv[kMaxPer / 2];
+#pragma unroll
+  for (int q = 0; q < kMaxPer / 2; ++q) {
+    const int p = sub + 8 * q;
+    wv[q] = p < pairs ? wr[p] : 0u;
+  }
+  float res[8];
+#pragma unroll
+  for (int n = 0; n < 8; ++n) {
+    res[n] = 0.f;
+    if (n >= N) continue;
+    const float2* xp =
+        reinterpret_cast<const float2*>(jo.x + (size_t)n * jo.x_ld);
+    float acc = 0.f;
+#pragma unroll
+    for (int q = 0; q < kMaxPer / 2; ++q) {
+      const int p = sub + 8 * q;
+      if (p < pairs) {
+        const float2 f = xp[p];
+        acc = dot2(wv[q], pack_h2(f.x, f.y), acc);
+      }
+    }
+    acc += dpp_f<0xB1>(acc);
+    acc += dpp_f<0x4E>(acc);
+    acc += dpp_f<0x141>(acc);
+    res[n] = acc;
+  }
+  if (live && sub == 0) {
+#pragma unroll
+    for (int n = 0; n < 8; ++n)
+      if (n < N) jo.y[(size_t)n * jo.y_ld + row] = epi_apply(res[n], jo.epi);
+  }
+}
+
+__device__ __forceinline__ void lora_run(const LoraJob& jo, int N, int gw,
+                                         int lane) {
+  const int lw = gw - jo.wave0;
+  if (lw * 8 >= jo.rows) return;
+  if (jo.in == 64 * 32) lora_wide<32>(jo, N, lw, lane);
+  else if (jo.in == 64 * 40) lora_wide<40>(jo, N, lw, lane);
+  else lora_narrow(jo, N, lw, lane);
+}
+
 __global__ void __launch_bounds__(256)
 lora_gemv_k(LoraJobs J) {
   const int lane = threadIdx.x & 63;
-  const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);     // global wave
+  const int gw = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(
+                                      threadIdx.x >> 6);
+  // the job is wave-uniform; each case reads the kernel-argument table
+  // with constant offsets (a dynamic index would copy it to scratch)
   int jb = 0;
-#pragma unroll
-  for (int q = 1; q < 4; ++q)
-    if (q < J.n_jobs && gw >= J.j[q].wave0) jb = q;
-  const LoraJob& jo = J.j[jb];
-  const int lw = gw - jo.wave0;
-  if (jo.in > 512) {
-    // wide: 64 lanes per row, 8 rows per wave, lane owns in/64 columns
-    const int per = jo.in >> 6;                          // multiple of 2
-    for (int rr = 0; rr < 8; ++rr) {
-      const int row = lw * 8 + rr;
-      if (row >= jo.rows) break;
-      const uint32_t* wr = reinterpret_cast<const uint32_t*>(
-          jo.W + (size_t)row * jo.in + lane * per);
-      for (int n = 0; n < J.N; ++n) {
-        const float* xp = jo.x + (size_t)n * jo.x_ld + lane * per;
-        float acc = 0.f;
-        for (int c = 0; c < per; c += 2)
-          acc = dot2(wr[c >> 1], pack_h2(xp[c], xp[c + 1]), acc);
-        acc = wave_sum_dpp(acc);
-        if (lane == 0)
-          jo.y[(size_t)n * jo.y_ld + row] = epi_apply(acc, jo.epi);
-      }
-    }
-  } else {
-    // narrow: 8 lanes per row, lane owns in/8 columns
-    const int sub = lane & 7, row = lw * 8 + (lane >> 3);
-    const int per = jo.in >> 3;                          // even
-    const bool live = row < jo.rows;
-    const uint32_t* wr = reinterpret_cast<const uint32_t*>(
-        jo.W + (size_t)(live ? row : 0) * jo.in + sub * per);
-    for (int n = 0; n < J.N; ++n) {
-      const float* xp = jo.x + (size_t)n * jo.x_ld + sub * per;
-      float acc = 0.f;
-      for (int c = 0; c < per; c += 2)
-        acc = dot2(wr[c >> 1], pack_h2(xp[c], xp[c + 1]), acc);
-      acc += dpp_f<0xB1>(acc);
-      acc += dpp_f<0x4E>(acc);
-      acc += dpp_f<0x141>(acc);
-      if (live && sub == 0)
-        jo.y[(size_t)n * jo.y_ld + row] = epi_apply(acc, jo.epi);
-    }
+  if (J.n_jobs > 1 && gw >= J.j[1].wave0) jb = 1;
+  if (J.n_jobs > 2 && gw >= J.j[2].wave0) jb = 2;
+  if (J.n_jobs > 3 && gw >= J.j[3].wave0) jb = 3;
+  switch (jb) {
+    case 0: lora_run(J.j[0], J.N, gw, lane); break;
+    case 1: lora_run(J.j[1], J.N, gw, lane); break;
+    case 2: lora_run(J.j[2], J.N, gw, lane); break;
+    default: lora_run(J.j[3], J.N, gw, lane); break;
   }
 }
 
@@ -99,8 +177,10 @@ extern "C" int rwkvq_lora_gemv(int n_jobs, const void* const* W,
   J.N = N;
   int waves = 0;
   for (int q = 0; q < n_jobs; ++q) {
+    const bool wide = in[q] == 64 * 32 || in[q] == 64 * 40;
     if (rows[q] <= 0 || in[q] <= 0 || in[q] % 16 ||
-        (in[q] > 512 && in[q] % 128) || x_ld[q] < in[q] || y_ld[q] < rows[q])
+        (!wide && in[q] > 8 * kMaxPer) || x_ld[q] < in[q] ||
+        y_ld[q] < rows[q])
       return RWKVQ_ERR_ARG;
     LoraJob& j = J.j[q];
     j.W = static_cast<const uint16_t*>(W[q]);

@@ -35,59 +35,107 @@ __device__ __forceinline__ float block_sum(float v, float* sh) {
   return s;
 }
 
-// Mean and rstd of one row of D floats (two-pass, as the reference).
-__device__ __forceinline__ void row_stats(const float* row, int D, float eps,
-                                          float* sh, float& mean,
+// Row kernels keep the row in registers: thread t owns columns t + 256 e,
+// e < kMaxE, so every load of a row is issued before the first use (a
+// loop over dependent global loads would pay the memory latency per
+// iteration).  D <= 256 * kMaxE.
+constexpr int kRowThreads = 256;
+constexpr int kMaxE = 16;
+
+__device__ __forceinline__ void load_row(const float* row, int D,
+                                         float (&v)[kMaxE]) {
+#pragma unroll
+  for (int e = 0; e < kMaxE; ++e) {
+    const int c = threadIdx.x + e * kRowThreads;
+    v[e] = c < D ? row[c] : 0.f;
+  }
+}
+
+// Mean and rstd of a register-resident row (two-pass, as the reference).
+__device__ __forceinline__ void row_stats(const float (&v)[kMaxE], int D,
+                                          float eps, float* sh, float& mean,
                                           float& rstd) {
   float s = 0.f;
-  for (int c = threadIdx.x; c < D; c += blockDim.x) s += row[c];
+#pragma unroll
+  for (int e = 0; e < kMaxE; ++e) s += v[e];
   mean = block_sum(s, sh) / (float)D;
   float q = 0.f;
-  for (int c = threadIdx.x; c < D; c += blockDim.x) {
-    float d = row[c] - mean;
+#pragma unroll
+  for (int e = 0; e < kMaxE; ++e) {
+    const int c = threadIdx.x + e * kRowThreads;
+    const float d = c < D ? v[e] - mean : 0.f;
     q += d * d;
   }
-  float var = block_sum(q, sh) / (float)D;
+  const float var = block_sum(q, sh) / (float)D;
   rstd = 1.f / sqrtf(var + eps);
 }
 
 // y = LN(x) row-wise (x and y may alias)
-__global__ void __launch_bounds__(256)
-layer_norm_k(const float* x, const float* w, const float* b, float* y, int D,
-             float eps) {
+__global__ void __launch_bounds__(kRowThreads)
+layer_norm_k(const float* x, const float* __restrict__ w,
+             const float* __restrict__ b, float* y, int D, float eps) {
   __shared__ float sh[16];
-  const float* xr = x + (size_t)blockIdx.x * D;
+  float v[kMaxE], cw[kMaxE], cb[kMaxE];
+  load_row(x + (size_t)blockIdx.x * D, D, v);
+  load_row(w, D, cw);
+  load_row(b, D, cb);
   float mean, rstd;
-  row_stats(xr, D, eps, sh, mean, rstd);
+  row_stats(v, D, eps, sh, mean, rstd);
   float* yr = y + (size_t)blockIdx.x * D;
-  for (int c = threadIdx.x; c < D; c += blockDim.x)
-    yr[c] = (xr[c] - mean) * rstd * w[c] + b[c];
+#pragma unroll
+  for (int e = 0; e < kMaxE; ++e) {
+    const int c = threadIdx.x + e * kRowThreads;
+    if (c < D) yr[c] = (v[e] - mean) * rstd * cw[e] + cb[e];
+  }
 }
 
 // LN + token shift + ncoef lerps for one token row (b, t):
 //   out[(b*T+t), k, :] = xn + (shift - xn) * coef[k, :]
 // shift = xn of (b, t-1), or prev[b] (zeros when prev is null) at t = 0.
-// new_prev[b] = xn of (b, T-1).  ln_out (optional) receives xn.
-__global__ void __launch_bounds__(256)
-shift_lerp_k(const float* x, const float* lw, const float* lb,
-             const float* prev, const float* coef, int ncoef, float* out,
-             float* new_prev, int T, int D) {
+// new_prev[b] = xn of (b, T-1).
+template <int NC>
+__global__ void __launch_bounds__(kRowThreads)
+shift_lerp_k(const float* __restrict__ x, const float* __restrict__ lw,
+             const float* __restrict__ lb, const float* __restrict__ prev,
+             const float* __restrict__ coef, float* __restrict__ out,
+             float* __restrict__ new_prev, int T, int D) {
   __shared__ float sh[16];
   const int row = blockIdx.x;           // b * T + t
   const int t = row % T, bb = row / T;
   const float* xr = x + (size_t)row * D;
+  float v[kMaxE], pv[kMaxE];
+  load_row(xr, D, v);
+  if (t > 0) load_row(xr - D, D, pv);
+  else if (prev) load_row(prev + (size_t)bb * D, D, pv);
+  // every load is issued before the first store: on this target the
+  // vector-memory counter covers stores too, so a load placed after a
+  // store would also wait for that store
+  float cw[kMaxE], cb[kMaxE], cf[NC][kMaxE];
+#pragma unroll
+  for (int e = 0; e < kMaxE; ++e) {
+    const int c = threadIdx.x + e * kRowThreads;
+    const bool in = c < D;
+    cw[e] = in ? lw[c] : 0.f;
+    cb[e] = in ? lb[c] : 0.f;
+#pragma unroll
+    for (int k = 0; k < NC; ++k) cf[k][e] = in ? coef[(size_t)k * D + c] : 0.f;
+  }
   float mean, rstd;
-  row_stats(xr, D, 1e-5f, sh, mean, rstd);
+  row_stats(v, D, 1e-5f, sh, mean, rstd);
   float pmean = 0.f, prstd = 0.f;
-  if (t > 0) row_stats(xr - D, D, 1e-5f, sh, pmean, prstd);
-  for (int c = threadIdx.x; c < D; c += blockDim.x) {
-    const float xn = (xr[c] - mean) * rstd * lw[c] + lb[c];
+  if (t > 0) row_stats(pv, D, 1e-5f, sh, pmean, prstd);
+#pragma unroll
+  for (int e = 0; e < kMaxE; ++e) {
+    const int c = threadIdx.x + e * kRowThreads;
+    if (c >= D) continue;
+    const float xn = (v[e] - mean) * rstd * cw[e] + cb[e];
     float sv;
-    if (t > 0) sv = (xr[c - D] - pmean) * prstd * lw[c] + lb[c];
-    else sv = prev ? prev[(size_t)bb * D + c] : 0.f;
+    if (t > 0) sv = (pv[e] - pmean) * prstd * cw[e] + cb[e];
+    else sv = prev ? pv[e] : 0.f;
     const float xx = sv - xn;
-    for (int k = 0; k < ncoef; ++k)
-      out[((size_t)row * ncoef + k) * D + c] = xn + xx * coef[(size_t)k * D + c];
+#pragma unroll
+    for (int k = 0; k < NC; ++k)
+      out[((size_t)row * NC + k) * D + c] = xn + xx * cf[k][e];
     if (t == T - 1 && new_prev) new_prev[(size_t)bb * D + c] = xn;
   }
 }
@@ -99,10 +147,14 @@ __device__ __forceinline__ float sigm(float v) { return 1.f / (1.f + __expf(-v))
 //   null on layer 0);  vfirst [N, D] written on layer 0, read otherwise.
 //   outputs w, kp, vp, aa, bb [N, D]
 __global__ void __launch_bounds__(256)
-wkv_prep_k(const float* rkv, const float* yw, const float* ya, const float* yv,
-           const float* w0, const float* a0, const float* v0, const float* k_k,
-           const float* k_a, float* vfirst, int layer0, float* wo, float* kpo,
-           float* vpo, float* aao, float* bbo, int D) {
+wkv_prep_k(const float* __restrict__ rkv, const float* __restrict__ yw,
+           const float* __restrict__ ya, const float* __restrict__ yv,
+           const float* __restrict__ w0, const float* __restrict__ a0,
+           const float* __restrict__ v0, const float* __restrict__ k_k,
+           const float* __restrict__ k_a, float* __restrict__ vfirst,
+           int layer0, float* __restrict__ wo, float* __restrict__ kpo,
+           float* __restrict__ vpo, float* __restrict__ aao,
+           float* __restrict__ bbo, int D) {
   const int n = blockIdx.y;
   const int c = blockIdx.x * blockDim.x + threadIdx.x;    // channel
   const size_t e = (size_t)n * D + c;
@@ -129,79 +181,128 @@ wkv_prep_k(const float* rkv, const float* yw, const float* ya, const float* yv,
 
 // WKV-7 recurrence.  Block = RB rows of one (batch, head) x L lanes per row;
 // lane (row i, part p) keeps S[i][p*C .. p*C+C) in registers (C = 64 / L).
-// The (S a) and (S r) row sums meet over the L lanes with DPP.
-template <int L>
-__global__ void __launch_bounds__(128)
-wkv_scan_k(const float* r, long r_ld, const float* w, const float* k,
-           const float* v, const float* aa, const float* bb, long ld,
-           const float* state_in, float* state, float* y, long y_ld, int T,
-           int H, int RB) {
-  constexpr int C = kHead / L;
+// The per-step vectors r, w, k, a, b of the head (64 columns each) and v of
+// the block's rows are staged through LDS in chunks of TC steps: the next
+// chunk is fetched into registers while the current one is consumed, so
+// the recurrence never waits on global memory.  The (S a) and (S r) row
+// sums meet over the L lanes with DPP.
+constexpr int kScanL = 16, kScanRB = 16, kScanTC = 32;
+constexpr int kScanThreads = kScanL * kScanRB;                 // 256
+constexpr int kVecF4 = kScanTC * 5 * (kHead / 4);              // float4 / chunk
+constexpr int kVecPerThread = kVecF4 / kScanThreads;           // 10
+constexpr int kVPerThread = kScanTC * kScanRB / kScanThreads;  // 2
+
+__global__ void __launch_bounds__(kScanThreads)
+wkv_scan_k(const float* __restrict__ r, long r_ld,
+           const float* __restrict__ w, const float* __restrict__ k,
+           const float* __restrict__ v, const float* __restrict__ aa,
+           const float* __restrict__ bb, long ld, const float* state_in,
+           float* state, float* __restrict__ y, long y_ld, int T, int H) {
+  constexpr int L = kScanL, C = kHead / L, RB = kScanRB, TC = kScanTC;
+  __shared__ float4 sv4[2][TC][5][kHead / 4];                   // 80 KiB
+  __shared__ float svv[2][TC][RB];
   const int nblk = kHead / RB;
   const int bh = blockIdx.x / nblk, rb = blockIdx.x % nblk;
   const int bi = bh / H, h = bh % H;
-  const int part = threadIdx.x % L;
-  const int i = rb * RB + threadIdx.x / L;                 // value row
+  const int tid = threadIdx.x;
+  const int part = tid % L;
+  const int il = tid / L;
+  const int i = rb * RB + il;                                  // value row
   const size_t soff = (((size_t)bi * H + h) * kHead + i) * kHead + part * C;
-  float* Sp = state + soff;
   float S[C];
-#pragma unroll
-  for (int c = 0; c < C; c += 4) {
-    float4 q = *reinterpret_cast<const float4*>(state_in + soff + c);
-    S[c] = q.x; S[c + 1] = q.y; S[c + 2] = q.z; S[c + 3] = q.w;
+  {
+    float4 q = *reinterpret_cast<const float4*>(state_in + soff);
+    S[0] = q.x; S[1] = q.y; S[2] = q.z; S[3] = q.w;
   }
-  const size_t col = (size_t)h * kHead + part * C;
-  for (int t = 0; t < T; ++t) {
-    const size_t tok = (size_t)bi * T + t;
-    const float* wp = w + tok * ld + col;
-    const float* kp = k + tok * ld + col;
-    const float* ap = aa + tok * ld + col;
-    const float* bp = bb + tok * ld + col;
-    const float* rp = r + tok * r_ld + col;
-    const float vi = v[tok * ld + (size_t)h * kHead + i];
-    float av[C], bv[C], wv[C], kv[C], rv[C];
+  const float* base[5] = {r, w, k, aa, bb};
+  const long lds[5] = {r_ld, ld, ld, ld, ld};
+  const size_t col0 = (size_t)h * kHead;
+  float4 stg[kVecPerThread];
+  float stv[kVPerThread];
+
+  auto fetch = [&](int t0) {
 #pragma unroll
-    for (int c = 0; c < C; c += 4) {
-      float4 q;
-      q = *reinterpret_cast<const float4*>(ap + c);
-      av[c] = q.x; av[c + 1] = q.y; av[c + 2] = q.z; av[c + 3] = q.w;
-      q = *reinterpret_cast<const float4*>(bp + c);
-      bv[c] = q.x; bv[c + 1] = q.y; bv[c + 2] = q.z; bv[c + 3] = q.w;
-      q = *reinterpret_cast<const float4*>(wp + c);
-      wv[c] = q.x; wv[c + 1] = q.y; wv[c + 2] = q.z; wv[c + 3] = q.w;
-      q = *reinterpret_cast<const float4*>(kp + c);
-      kv[c] = q.x; kv[c + 1] = q.y; kv[c + 2] = q.z; kv[c + 3] = q.w;
-      q = *reinterpret_cast<const float4*>(rp + c);
-      rv[c] = q.x; rv[c + 1] = q.y; rv[c + 2] = q.z; rv[c + 3] = q.w;
+    for (int m = 0; m < kVecPerThread; ++m) {
+      const int e = tid + m * kScanThreads;          // over [TC][5][16]
+      const int f4 = e % (kHead / 4), q = (e / (kHead / 4)) % 5,
+                tt = e / (5 * (kHead / 4));
+      const int t = min(t0 + tt, T - 1);
+      const size_t tok = (size_t)bi * T + t;
+      stg[m] = *reinterpret_cast<const float4*>(base[q] + tok * lds[q] +
+                                                col0 + 4 * f4);
     }
-    float sa = 0.f;
 #pragma unroll
-    for (int c = 0; c < C; ++c) sa += S[c] * av[c];
-    if (L >= 2) sa += dpp_f<0xB1>(sa);     // xor 1
-    if (L >= 4) sa += dpp_f<0x4E>(sa);     // xor 2
-    if (L >= 8) sa += dpp_f<0x141>(sa);    // half-row mirror
-    float yv = 0.f;
-#pragma unroll
-    for (int c = 0; c < C; ++c) {
-      S[c] = S[c] * wv[c] + sa * bv[c] + vi * kv[c];
-      yv += S[c] * rv[c];
+    for (int m = 0; m < kVPerThread; ++m) {
+      const int e = tid + m * kScanThreads;          // over [TC][RB]
+      const int rr = e % RB, tt = e / RB;
+      const int t = min(t0 + tt, T - 1);
+      stv[m] = v[((size_t)bi * T + t) * ld + col0 + rb * RB + rr];
     }
-    if (L >= 2) yv += dpp_f<0xB1>(yv);
-    if (L >= 4) yv += dpp_f<0x4E>(yv);
-    if (L >= 8) yv += dpp_f<0x141>(yv);
-    if (part == 0) y[tok * y_ld + (size_t)h * kHead + i] = yv;
+  };
+  auto stash = [&](int buf) {
+#pragma unroll
+    for (int m = 0; m < kVecPerThread; ++m) {
+      const int e = tid + m * kScanThreads;
+      const int f4 = e % (kHead / 4), q = (e / (kHead / 4)) % 5,
+                tt = e / (5 * (kHead / 4));
+      sv4[buf][tt][q][f4] = stg[m];
+    }
+#pragma unroll
+    for (int m = 0; m < kVPerThread; ++m) {
+      const int e = tid + m * kScanThreads;
+      svv[buf][e / RB][e % RB] = stv[m];
+    }
+  };
+
+  fetch(0);
+  stash(0);
+  __syncthreads();
+  int buf = 0;
+  for (int t0 = 0; t0 < T; t0 += TC) {
+    const bool more = t0 + TC < T;
+    if (more) fetch(t0 + TC);                        // in flight meanwhile
+    const int n = min(TC, T - t0);
+    for (int tt = 0; tt < n; ++tt) {
+      const float4 rv = sv4[buf][tt][0][part];
+      const float4 wv = sv4[buf][tt][1][part];
+      const float4 kv = sv4[buf][tt][2][part];
+      const float4 av = sv4[buf][tt][3][part];
+      const float4 bv = sv4[buf][tt][4][part];
+      const float vi = svv[buf][tt][il];
+      float sa = S[0] * av.x + S[1] * av.y + S[2] * av.z + S[3] * av.w;
+      sa += dpp_f<0xB1>(sa);      // xor 1
+      sa += dpp_f<0x4E>(sa);      // xor 2
+      sa += dpp_f<0x141>(sa);     // half-row mirror (8)
+      sa += dpp_f<0x140>(sa);     // row mirror (16)
+      S[0] = S[0] * wv.x + sa * bv.x + vi * kv.x;
+      S[1] = S[1] * wv.y + sa * bv.y + vi * kv.y;
+      S[2] = S[2] * wv.z + sa * bv.z + vi * kv.z;
+      S[3] = S[3] * wv.w + sa * bv.w + vi * kv.w;
+      float yv = S[0] * rv.x + S[1] * rv.y + S[2] * rv.z + S[3] * rv.w;
+      yv += dpp_f<0xB1>(yv);
+      yv += dpp_f<0x4E>(yv);
+      yv += dpp_f<0x141>(yv);
+      yv += dpp_f<0x140>(yv);
+      if (part == 0)
+        y[((size_t)bi * T + t0 + tt) * y_ld + col0 + i] = yv;
+    }
+    if (more) {
+      stash(buf ^ 1);
+      __syncthreads();
+      buf ^= 1;
+    }
   }
-#pragma unroll
-  for (int c = 0; c < C; c += 4)
-    *reinterpret_cast<float4*>(Sp + c) = make_float4(S[c], S[c + 1], S[c + 2],
-                                                     S[c + 3]);
+  *reinterpret_cast<float4*>(state + soff) = make_float4(S[0], S[1], S[2],
+                                                         S[3]);
 }
 
 // Group norm per head + bonus + gate.  One wave = one (token, head).
 __global__ void __launch_bounds__(256)
-wkv_tail_k(const float* y, const float* rkv, const float* kp, const float* vp,
-           const float* g, const float* r_k, const float* lnw,
-           const float* lnb, float* out, int D) {
+wkv_tail_k(const float* __restrict__ y, const float* __restrict__ rkv,
+           const float* __restrict__ kp, const float* __restrict__ vp,
+           const float* __restrict__ g, const float* __restrict__ r_k,
+           const float* __restrict__ lnw, const float* __restrict__ lnb,
+           float* __restrict__ out, int D) {
   const int n = blockIdx.y;
   const int c = blockIdx.x * blockDim.x + threadIdx.x;
   const size_t e = (size_t)n * D + c;
@@ -215,6 +316,104 @@ wkv_tail_k(const float* y, const float* rkv, const float* kp, const float* vp,
   out[e] = ((nrm * lnw[c] + lnb[c]) + dp * vp[e]) * g[e];
 }
 
+// Decode (T = 1) time-mix core for one (sequence, head) per block: the
+// per-channel WKV inputs, one recurrence step and the group-norm / bonus /
+// gate tail in one launch.  256 threads: thread (row i = tid / 4, part
+// p = tid % 4) owns S[i][16 p .. 16 p + 16); wave 0 handles the per-channel
+// work of the head's 64 channels.
+__global__ void __launch_bounds__(256)
+wkv_decode_k(const float* __restrict__ rkv, const float* __restrict__ yw,
+             const float* __restrict__ ya, const float* __restrict__ yv,
+             const float* __restrict__ g, const float* __restrict__ w0,
+             const float* __restrict__ a0, const float* __restrict__ v0,
+             const float* __restrict__ k_k, const float* __restrict__ k_a,
+             const float* __restrict__ r_k, const float* __restrict__ lnw,
+             const float* __restrict__ lnb, float* __restrict__ vfirst,
+             int layer0, const float* state_in, float* state_out,
+             float* __restrict__ out, int H) {
+  constexpr int P = 4, C = kHead / P;
+  __shared__ float4 s_w[kHead / 4], s_k[kHead / 4], s_a[kHead / 4],
+      s_b[kHead / 4], s_r[kHead / 4];
+  __shared__ float s_v[kHead], s_y[kHead];
+  __shared__ float s_dp;
+  const int bi = blockIdx.x / H, h = blockIdx.x % H;
+  const int D = H * kHead;
+  const int tid = threadIdx.x;
+  const int i = tid / P, part = tid % P;
+  // state row slice: issue the loads first, they do not depend on phase 1
+  const size_t soff = (((size_t)bi * H + h) * kHead + i) * kHead + part * C;
+  float S[C];
+#pragma unroll
+  for (int c = 0; c < C; c += 4) {
+    float4 q = *reinterpret_cast<const float4*>(state_in + soff + c);
+    S[c] = q.x; S[c + 1] = q.y; S[c + 2] = q.z; S[c + 3] = q.w;
+  }
+  float vp = 0.f, gc = 0.f, lw = 0.f, lb = 0.f;
+  if (tid < kHead) {
+    const int c = h * kHead + tid;
+    const size_t e = (size_t)bi * D + c;
+    const float r = rkv[(size_t)bi * 3 * D + c];
+    const float k = rkv[(size_t)bi * 3 * D + D + c];
+    float v = rkv[(size_t)bi * 3 * D + 2 * D + c];
+    const float wv = __expf(-0.606531f * sigm(yw[e] + w0[c]));
+    const float av = sigm(ya[e] + a0[c]);
+    const float kkr = k * k_k[c];
+    const float kk = kkr / sqrtf(wave_sum_dpp(kkr * kkr) + 1e-12f);
+    const float kp = k * (1.f + (av - 1.f) * k_a[c]);
+    gc = g[e]; lw = lnw[c]; lb = lnb[c];
+    const float rkc = r_k[c];
+    if (!layer0) v = v + (vfirst[e] - v) * sigm(yv[e] + v0[c]);
+    else vfirst[e] = v;
+    const float dp = wave_sum_dpp(r * kp * rkc);
+    reinterpret_cast<float*>(s_w)[tid] = wv;
+    reinterpret_cast<float*>(s_k)[tid] = kp;
+    reinterpret_cast<float*>(s_a)[tid] = -kk;
+    reinterpret_cast<float*>(s_b)[tid] = kk * av;
+    reinterpret_cast<float*>(s_r)[tid] = r;
+    s_v[tid] = v;
+    if (tid == 0) s_dp = dp;
+    vp = v;
+  }
+  __syncthreads();
+  const float vi = s_v[i];
+  float sa = 0.f;
+#pragma unroll
+  for (int c = 0; c < C; c += 4) {
+    const float4 a4 = s_a[part * (C / 4) + c / 4];
+    sa += S[c] * a4.x + S[c + 1] * a4.y + S[c + 2] * a4.z + S[c + 3] * a4.w;
+  }
+  sa += dpp_f<0xB1>(sa);
+  sa += dpp_f<0x4E>(sa);
+  float yv2 = 0.f;
+#pragma unroll
+  for (int c = 0; c < C; c += 4) {
+    const int q = part * (C / 4) + c / 4;
+    const float4 w4 = s_w[q], b4 = s_b[q], k4 = s_k[q], r4 = s_r[q];
+    S[c] = S[c] * w4.x + sa * b4.x + vi * k4.x;
+    S[c + 1] = S[c + 1] * w4.y + sa * b4.y + vi * k4.y;
+    S[c + 2] = S[c + 2] * w4.z + sa * b4.z + vi * k4.z;
+    S[c + 3] = S[c + 3] * w4.w + sa * b4.w + vi * k4.w;
+    yv2 += S[c] * r4.x + S[c + 1] * r4.y + S[c + 2] * r4.z + S[c + 3] * r4.w;
+  }
+  yv2 += dpp_f<0xB1>(yv2);
+  yv2 += dpp_f<0x4E>(yv2);
+#pragma unroll
+  for (int c = 0; c < C; c += 4)
+    *reinterpret_cast<float4*>(state_out + soff + c) =
+        make_float4(S[c], S[c + 1], S[c + 2], S[c + 3]);
+  if (part == 0) s_y[i] = yv2;
+  __syncthreads();
+  if (tid < kHead) {
+    const float yy = s_y[tid];
+    const float mean = wave_sum_dpp(yy) * (1.f / kHead);
+    const float dv = yy - mean;
+    const float var = wave_sum_dpp(dv * dv) * (1.f / kHead);
+    const float nrm = dv / sqrtf(var + 64e-5f);
+    out[(size_t)bi * D + h * kHead + tid] =
+        ((nrm * lw + lb) + s_dp * vp) * gc;
+  }
+}
+
 inline int ok_launch() {
   return hipGetLastError() == hipSuccess ? RWKVQ_OK : RWKVQ_ERR_LAUNCH;
 }
@@ -225,7 +424,7 @@ extern "C" {
 
 int rwkvq_layer_norm(const float* x, const float* w, const float* b, float* y,
                      int rows, int D, float eps, void* stream) {
-  if (rows <= 0 || D <= 0) return RWKVQ_ERR_ARG;
+  if (rows <= 0 || D <= 0 || D > kRowThreads * kMaxE) return RWKVQ_ERR_ARG;
   hipLaunchKernelGGL(layer_norm_k, dim3(rows), dim3(256), 0,
                      (hipStream_t)stream, x, w, b, y, D, eps);
   return ok_launch();
@@ -235,11 +434,17 @@ int rwkvq_shift_lerp(const float* x, const float* ln_w, const float* ln_b,
                      const float* prev, const float* coef, int ncoef,
                      float* out, float* new_prev, int B, int T, int D,
                      void* stream) {
-  if (B <= 0 || T <= 0 || D <= 0 || ncoef <= 0 || ncoef > 8)
+  if (B <= 0 || T <= 0 || D <= 0 || D > kRowThreads * kMaxE ||
+      (ncoef != 1 && ncoef != 6))
     return RWKVQ_ERR_ARG;
-  hipLaunchKernelGGL(shift_lerp_k, dim3(B * T), dim3(256), 0,
-                     (hipStream_t)stream, x, ln_w, ln_b, prev, coef, ncoef,
-                     out, new_prev, T, D);
+  if (ncoef == 6)
+    hipLaunchKernelGGL(shift_lerp_k<6>, dim3(B * T), dim3(kRowThreads), 0,
+                       (hipStream_t)stream, x, ln_w, ln_b, prev, coef, out,
+                       new_prev, T, D);
+  else
+    hipLaunchKernelGGL(shift_lerp_k<1>, dim3(B * T), dim3(kRowThreads), 0,
+                       (hipStream_t)stream, x, ln_w, ln_b, prev, coef, out,
+                       new_prev, T, D);
   return ok_launch();
 }
 
@@ -266,11 +471,10 @@ int rwkvq_wkv7_scan(const float* r, long r_ld, const float* w, const float* k,
   if (B <= 0 || T <= 0 || H <= 0 || head_size != kHead || ld < H * kHead ||
       r_ld < H * kHead || y_ld < H * kHead || (r_ld & 3) || (ld & 3))
     return RWKVQ_ERR_ARG;
-  constexpr int L = 8, RB = 16;
-  hipLaunchKernelGGL((wkv_scan_k<L>), dim3(B * H * (kHead / RB)),
-                     dim3(RB * L), 0, (hipStream_t)stream, r, r_ld, w, k, v,
-                     a, b, ld, state_in ? state_in : state_out, state_out, y,
-                     y_ld, T, H, RB);
+  hipLaunchKernelGGL(wkv_scan_k, dim3(B * H * (kHead / kScanRB)),
+                     dim3(kScanThreads), 0, (hipStream_t)stream, r, r_ld, w,
+                     k, v, a, b, ld, state_in ? state_in : state_out,
+                     state_out, y, y_ld, T, H);
   return ok_launch();
 }
 
@@ -282,6 +486,22 @@ int rwkvq_wkv_tail(const float* y, const float* rkv, const float* kp,
   hipLaunchKernelGGL(wkv_tail_k, dim3(D / 256, N), dim3(256), 0,
                      (hipStream_t)stream, y, rkv, kp, vp, g, r_k, ln_w, ln_b,
                      out, D);
+  return ok_launch();
+}
+
+int rwkvq_wkv7_decode(const float* rkv, const float* yw, const float* ya,
+                      const float* yv, const float* g, const float* w0,
+                      const float* a0, const float* v0, const float* k_k,
+                      const float* k_a, const float* r_k, const float* ln_w,
+                      const float* ln_b, float* v_first, int layer0,
+                      const float* state_in, float* state_out, float* out,
+                      int B, int H, int head_size, void* stream) {
+  if (B <= 0 || H <= 0 || head_size != kHead || (!layer0 && (!yv || !v0)))
+    return RWKVQ_ERR_ARG;
+  hipLaunchKernelGGL(wkv_decode_k, dim3(B * H), dim3(256), 0,
+                     (hipStream_t)stream, rkv, yw, ya, yv, g, w0, a0, v0, k_k,
+                     k_a, r_k, ln_w, ln_b, v_first, layer0,
+                     state_in ? state_in : state_out, state_out, out, H);
   return ok_launch();
 }
 

@@ -385,24 +385,19 @@ class QuantRWKV7:
                     yv.copy_(tmp)
             tm.run_lora(wk)
             layer0 = 1 if li == 0 else 0
-            _lib.call("rwkvq_wkv_prep", _lib.ptr(wk.rkv),
-                      _lib.ptr(wk.yl["w"]), _lib.ptr(wk.yl["a"]),
-                      None if layer0 else _lib.ptr(wk.yl["v"]),
-                      _lib.ptr(tm.w0), _lib.ptr(tm.a0), _lib.ptr(tm.v0),
-                      _lib.ptr(tm.k_k), _lib.ptr(tm.k_a),
-                      _lib.ptr(wk.v_first), layer0, _lib.ptr(wk.w),
-                      _lib.ptr(wk.kp), _lib.ptr(wk.vp), _lib.ptr(wk.aa),
-                      _lib.ptr(wk.bb), N, C, self.head_size, st)
-            _lib.call("rwkvq_wkv7_scan", _lib.ptr(wk.rkv), 3 * C,
-                      _lib.ptr(wk.w), _lib.ptr(wk.kp), _lib.ptr(wk.vp),
-                      _lib.ptr(wk.aa), _lib.ptr(wk.bb), C, _lib.ptr(wkv_in),
-                      _lib.ptr(wkv_out), _lib.ptr(wk.y), C, B, T, H,
-                      self.head_size, st)
-            _lib.call("rwkvq_wkv_tail", _lib.ptr(wk.y), _lib.ptr(wk.rkv),
-                      _lib.ptr(wk.kp), _lib.ptr(wk.vp), _lib.ptr(wk.yl["g"]),
-                      _lib.ptr(tm.r_k), _lib.ptr(tm.ln_x_w),
-                      _lib.ptr(tm.ln_x_b), _lib.ptr(wk.o), N, C,
-                      self.head_size, st)
+            if T == 1:
+                _lib.call("rwkvq_wkv7_decode", _lib.ptr(wk.rkv),
+                          _lib.ptr(wk.yl["w"]), _lib.ptr(wk.yl["a"]),
+                          None if layer0 else _lib.ptr(wk.yl["v"]),
+                          _lib.ptr(wk.yl["g"]), _lib.ptr(tm.w0),
+                          _lib.ptr(tm.a0), _lib.ptr(tm.v0), _lib.ptr(tm.k_k),
+                          _lib.ptr(tm.k_a), _lib.ptr(tm.r_k),
+                          _lib.ptr(tm.ln_x_w), _lib.ptr(tm.ln_x_b),
+                          _lib.ptr(wk.v_first), layer0, _lib.ptr(wkv_in),
+                          _lib.ptr(wkv_out), _lib.ptr(wk.o), B, H,
+                          self.head_size, st)
+            else:
+                self._wkv_seq(tm, wk, wkv_in, wkv_out, layer0, B, T, st)
             _apply(tm.o_proj, wk.o, x, _lib.EPI_ADD)
             _lib.call("rwkvq_shift_lerp", _lib.ptr(x), _lib.ptr(blk.ln2_w),
                       _lib.ptr(blk.ln2_b), _lib.ptr(cshift),
@@ -412,6 +407,25 @@ class QuantRWKV7:
             _apply(cm.value, wk.hk, x, _lib.EPI_ADD)
         _lib.call("rwkvq_layer_norm", _lib.ptr(x), _lib.ptr(self.ln_out_w),
                   _lib.ptr(self.ln_out_b), _lib.ptr(wk.xo), N, C, 1e-5, st)
+
+    def _wkv_seq(self, tm, wk, wkv_in, wkv_out, layer0, B, T, st):
+        """T > 1: per-channel inputs, chunked scan, tail (three launches)."""
+        N, C, H = B * T, self.n_embd, self.n_head
+        _lib.call("rwkvq_wkv_prep", _lib.ptr(wk.rkv), _lib.ptr(wk.yl["w"]),
+                  _lib.ptr(wk.yl["a"]),
+                  None if layer0 else _lib.ptr(wk.yl["v"]), _lib.ptr(tm.w0),
+                  _lib.ptr(tm.a0), _lib.ptr(tm.v0), _lib.ptr(tm.k_k),
+                  _lib.ptr(tm.k_a), _lib.ptr(wk.v_first), layer0,
+                  _lib.ptr(wk.w), _lib.ptr(wk.kp), _lib.ptr(wk.vp),
+                  _lib.ptr(wk.aa), _lib.ptr(wk.bb), N, C, self.head_size, st)
+        _lib.call("rwkvq_wkv7_scan", _lib.ptr(wk.rkv), 3 * C, _lib.ptr(wk.w),
+                  _lib.ptr(wk.kp), _lib.ptr(wk.vp), _lib.ptr(wk.aa),
+                  _lib.ptr(wk.bb), C, _lib.ptr(wkv_in), _lib.ptr(wkv_out),
+                  _lib.ptr(wk.y), C, B, T, H, self.head_size, st)
+        _lib.call("rwkvq_wkv_tail", _lib.ptr(wk.y), _lib.ptr(wk.rkv),
+                  _lib.ptr(wk.kp), _lib.ptr(wk.vp), _lib.ptr(wk.yl["g"]),
+                  _lib.ptr(tm.r_k), _lib.ptr(tm.ln_x_w), _lib.ptr(tm.ln_x_b),
+                  _lib.ptr(wk.o), N, C, self.head_size, st)
 
     def _new_states(self, B):
         H, S, C = self.n_head, self.head_size, self.n_embd

@@ -137,3 +137,38 @@ def test_decode_continues_prefill_state(toy):
                                    model.init_state(1))
     lg, _ = model.step(torch.from_numpy(idx[:, 8:]), st)
     assert _maxabs(lg.cpu().numpy()[:, 0], ref[:, 8]) < 1e-2
+
+
+@pytest.mark.parametrize("layer0", [1, 0])
+def test_fused_decode_core_equals_three_kernels(layer0):
+    """rwkvq_wkv7_decode == wkv_prep + wkv7_scan(T=1) + wkv_tail."""
+    B, H = 3, 32
+    D = H * 64
+    g = torch.Generator().manual_seed(21 + layer0)
+    mk = lambda *s, sc=1.0: (torch.randn(*s, generator=g) * sc).cuda()
+    rkv, yw, ya, yv, gg = mk(B, 3, D), mk(B, D), mk(B, D), mk(B, D), mk(B, D)
+    w0, a0, v0 = mk(D, sc=0.5), mk(D, sc=0.5), mk(D, sc=0.5)
+    k_k, k_a, r_k = mk(D).abs(), torch.rand(D).cuda(), mk(D, sc=0.1)
+    lnw, lnb = mk(D), mk(D, sc=0.1)
+    vf1, vf2 = mk(B, D), None
+    vf2 = vf1.clone()
+    st0 = mk(B, H, 64, 64, sc=0.05)
+    st_a, st_b = torch.empty_like(st0), torch.empty_like(st0)
+    out_a, out_b = torch.empty(B, D).cuda(), torch.empty(B, D).cuda()
+    P = _lib.ptr
+    s = _lib.stream_handle()
+    _lib.call("rwkvq_wkv7_decode", P(rkv), P(yw), P(ya), P(yv), P(gg), P(w0),
+              P(a0), P(v0), P(k_k), P(k_a), P(r_k), P(lnw), P(lnb), P(vf1),
+              layer0, P(st0), P(st_a), P(out_a), B, H, 64, s)
+    w, kp, vp, aa, bb, y = (torch.empty(B, D).cuda() for _ in range(6))
+    _lib.call("rwkvq_wkv_prep", P(rkv), P(yw), P(ya), P(yv), P(w0), P(a0),
+              P(v0), P(k_k), P(k_a), P(vf2), layer0, P(w), P(kp), P(vp),
+              P(aa), P(bb), B, D, 64, s)
+    _lib.call("rwkvq_wkv7_scan", P(rkv), 3 * D, P(w), P(kp), P(vp), P(aa),
+              P(bb), D, P(st0), P(st_b), P(y), D, B, 1, H, 64, s)
+    _lib.call("rwkvq_wkv_tail", P(y), P(rkv), P(kp), P(vp), P(gg), P(r_k),
+              P(lnw), P(lnb), P(out_b), B, D, 64, s)
+    rel = lambda a, b: float((a - b).abs().max() / b.abs().max())
+    assert rel(st_a, st_b) < 1e-5
+    assert rel(out_a, out_b) < 1e-5
+    assert torch.equal(vf1, vf2)
