@@ -105,6 +105,16 @@ int rwkvq_dequant_asym_f32(const uint8_t* codes, const float* scale,
                            const float* mn, int gs, int rows, int in,
                            float* w, int ld, void* stream);
 
+/* Dense fp16 expansion for the prefill GEMM: out[r, c] = f16(dequant(W)[r, c])
+ * where dequant is the bit-exact fp32 formula above (one rounding).
+ * fmt 0/1/2 = sb6@4/5/6 (q = nib, hb, rec), 3/4 = sym@6/8 (q = codes, hb,
+ * qs, d), 5 = rtn@8 (q = codes, d = scale).  ld % 8 == 0.
+ * Replaces: GwQuantLinear._dequant_w / SymQuantLinear._dequant_w(fp16)
+ *   (reference: quant_linear_gw.py:821-840; quant_linear_sym.py:275-363). */
+int rwkvq_dequant_f16(int fmt, const uint8_t* q, const uint32_t* hb,
+                      const uint8_t* rec, const int8_t* qs, const uint16_t* d,
+                      int rows, int in, uint16_t* out, int ld, void* stream);
+
 /* Row gather of a packed matrix into fp32 (the embedding lookup):
  * out[o, :] = dequant(W)[min(max(idx[o], 0), src_rows - 1), :], o < n_idx.
  * kind 0 = sb6 (q = nib, hb, aux0 = rec), 1 = sym (q = codes, hb,

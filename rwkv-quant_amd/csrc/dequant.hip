@@ -121,6 +121,141 @@ __global__ void dq_asym(const uint8_t* codes, const float* scale,
   w[(size_t)row * ld + c] = (float)codes[t] * scale[b] + mn[b];
 }
 
+// ---- wide dequant for the prefill GEMM operands -------------------------
+// One thread per (row, 32-column group): 16-byte loads of the packed fields,
+// the same fp32 arithmetic as the bit-exact kernels above, then one
+// rounding to the output type and 16-byte stores in natural column order.
+// fp16 output is therefore exactly f16(the bit-exact fp32 dequant).
+enum DqFmt { DQ_SB6_4 = 0, DQ_SB6_5, DQ_SB6_6, DQ_SYM6, DQ_SYM8, DQ_RTN8 };
+
+template <int FMT>
+__device__ __forceinline__ void group_values(
+    const uint8_t* __restrict__ q, const uint32_t* __restrict__ hb,
+    const uint8_t* __restrict__ rec, const int8_t* __restrict__ qsp,
+    const uint16_t* __restrict__ dp, int in, int row, int g, float (&w)[32]) {
+  const int ng = in >> 5, nsb = in >> 8;
+  if (FMT == DQ_SYM8 || FMT == DQ_RTN8) {
+    const uint8_t* p = q + (size_t)row * in + (size_t)g * 32;
+    const uint4 a = *reinterpret_cast<const uint4*>(p);
+    const uint4 b = *reinterpret_cast<const uint4*>(p + 16);
+    const uint32_t wd[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    float sA, sB;
+    if (FMT == DQ_RTN8) {
+      sA = sB = f16_bits_to_f32(dp[row]);
+    } else {
+      const float d = f16_bits_to_f32(dp[(size_t)row * nsb + (g >> 3)]);
+      const uint16_t q2 =
+          *reinterpret_cast<const uint16_t*>(qsp + (size_t)row * (in >> 4) + 2 * g);
+      sA = f16_round((float)(int8_t)(q2 & 0xFF) * d);
+      sB = f16_round((float)(int8_t)(q2 >> 8) * d);
+    }
+#pragma unroll
+    for (int c = 0; c < 32; ++c) {
+      const int8_t code = (int8_t)((wd[c >> 2] >> (8 * (c & 3))) & 0xFF);
+      w[c] = (float)code * (c < 16 ? sA : sB);
+    }
+    return;
+  }
+  const uint4 nb = *reinterpret_cast<const uint4*>(q + ((size_t)row * ng + g) * 16);
+  const uint32_t nw[4] = {nb.x, nb.y, nb.z, nb.w};
+  uint32_t h0 = 0, h1 = 0;
+  if (FMT == DQ_SB6_5) h0 = hb[(size_t)row * ng + g];
+  if (FMT == DQ_SB6_6 || FMT == DQ_SYM6) {
+    const uint2 hh = *reinterpret_cast<const uint2*>(hb + ((size_t)row * ng + g) * 2);
+    h0 = hh.x; h1 = hh.y;
+  }
+  int code[32];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {            // nibble byte i
+    const uint32_t byte = (nw[i >> 2] >> (8 * (i & 3))) & 0xFF;
+    int c0, c1;
+    if (FMT == DQ_SYM6) { c0 = i < 8 ? i : i + 8; c1 = c0 + 8; }
+    else { c0 = i; c1 = i + 16; }
+    uint32_t lo = byte & 15, hi = byte >> 4;
+    if (FMT == DQ_SB6_5) {
+      lo |= ((h0 >> c0) & 1) << 4;
+      hi |= ((h0 >> c1) & 1) << 4;
+    } else if (FMT == DQ_SB6_6 || FMT == DQ_SYM6) {
+      const uint32_t H = i < 8 ? h0 : h1;
+      const int sh = 2 * (i & 7);
+      lo |= ((H >> sh) & 3) << 4;
+      hi |= ((H >> (sh + 16)) & 3) << 4;
+    }
+    code[c0] = (int)lo;
+    code[c1] = (int)hi;
+  }
+  if (FMT == DQ_SYM6) {
+    const float d = f16_bits_to_f32(dp[(size_t)row * nsb + (g >> 3)]);
+    const uint16_t q2 =
+        *reinterpret_cast<const uint16_t*>(qsp + (size_t)row * (in >> 4) + 2 * g);
+    const float sA = f16_round((float)(int8_t)(q2 & 0xFF) * d);
+    const float sB = f16_round((float)(int8_t)(q2 >> 8) * d);
+#pragma unroll
+    for (int c = 0; c < 32; ++c) w[c] = (float)(code[c] - 32) * (c < 16 ? sA : sB);
+    return;
+  }
+  // sb6: superblock record
+  const uint4 rc = *reinterpret_cast<const uint4*>(rec + ((size_t)row * nsb + (g >> 3)) * 16);
+  const uint64_t s0 = (uint64_t)rc.x | ((uint64_t)(rc.y & 0xFFFF) << 32);
+  const uint64_t s1 = (uint64_t)(rc.y >> 16) | ((uint64_t)rc.z << 16);
+  const int kb = g & 7;
+  const uint32_t qsv = (uint32_t)(s0 >> (6 * kb)) & 63u;
+  const int qmv = (int)((uint32_t)(s1 >> (6 * kb)) & 63u) - 31;
+  const float d = f16_bits_to_f32(rc.w & 0xFFFF);
+  const float dm = f16_bits_to_f32(rc.w >> 16);
+  const float sc = fmaxf(f16_round((float)qsv * d), 1e-8f);
+  const float mn = f16_round((float)qmv * dm);
+#pragma unroll
+  for (int c = 0; c < 32; ++c) w[c] = (float)code[c] * sc + mn;
+}
+
+template <int FMT, typename OutT>
+__global__ void __launch_bounds__(256)
+dq_wide_k(const uint8_t* __restrict__ q, const uint32_t* __restrict__ hb,
+          const uint8_t* __restrict__ rec, const int8_t* __restrict__ qsp,
+          const uint16_t* __restrict__ dp, int rows, int in,
+          OutT* __restrict__ out, int ld) {
+  const int ng = in >> 5;
+  const long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (long)rows * ng) return;
+  const int row = (int)(t / ng), g = (int)(t % ng);
+  float w[32];
+  group_values<FMT>(q, hb, rec, qsp, dp, in, row, g, w);
+  OutT* o = out + (size_t)row * ld + (size_t)g * 32;
+  if constexpr (sizeof(OutT) == 2) {
+    uint32_t pk[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) pk[i] = pack_h2(w[2 * i], w[2 * i + 1]);
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+      reinterpret_cast<uint4*>(o)[v] =
+          make_uint4(pk[4 * v], pk[4 * v + 1], pk[4 * v + 2], pk[4 * v + 3]);
+  } else {
+#pragma unroll
+    for (int v = 0; v < 8; ++v)
+      reinterpret_cast<float4*>(o)[v] =
+          make_float4(w[4 * v], w[4 * v + 1], w[4 * v + 2], w[4 * v + 3]);
+  }
+}
+
+template <typename OutT>
+int launch_wide(int fmt, const uint8_t* q, const uint32_t* hb,
+                const uint8_t* rec, const int8_t* qs, const uint16_t* d,
+                int rows, int in, OutT* out, int ld, hipStream_t s) {
+  const long n = (long)rows * (in / 32);
+  const dim3 grid((unsigned)((n + 255) / 256)), block(256);
+  switch (fmt) {
+    case DQ_SB6_4: hipLaunchKernelGGL((dq_wide_k<DQ_SB6_4, OutT>), grid, block, 0, s, q, hb, rec, qs, d, rows, in, out, ld); break;
+    case DQ_SB6_5: hipLaunchKernelGGL((dq_wide_k<DQ_SB6_5, OutT>), grid, block, 0, s, q, hb, rec, qs, d, rows, in, out, ld); break;
+    case DQ_SB6_6: hipLaunchKernelGGL((dq_wide_k<DQ_SB6_6, OutT>), grid, block, 0, s, q, hb, rec, qs, d, rows, in, out, ld); break;
+    case DQ_SYM6: hipLaunchKernelGGL((dq_wide_k<DQ_SYM6, OutT>), grid, block, 0, s, q, hb, rec, qs, d, rows, in, out, ld); break;
+    case DQ_SYM8: hipLaunchKernelGGL((dq_wide_k<DQ_SYM8, OutT>), grid, block, 0, s, q, hb, rec, qs, d, rows, in, out, ld); break;
+    case DQ_RTN8: hipLaunchKernelGGL((dq_wide_k<DQ_RTN8, OutT>), grid, block, 0, s, q, hb, rec, qs, d, rows, in, out, ld); break;
+    default: return RWKVQ_ERR_ARG;
+  }
+  return hipGetLastError() == hipSuccess ? RWKVQ_OK : RWKVQ_ERR_LAUNCH;
+}
+
 inline dim3 grid_for(long n, int bs) { return dim3((unsigned)((n + bs - 1) / bs)); }
 
 }  // namespace
@@ -203,6 +338,17 @@ int rwkvq_gather_rows_f32(int kind, int bits, const uint8_t* q,
     return RWKVQ_ERR_ARG;
   }
   return hipGetLastError() == hipSuccess ? RWKVQ_OK : RWKVQ_ERR_LAUNCH;
+}
+
+int rwkvq_dequant_f16(int fmt, const uint8_t* q, const uint32_t* hb,
+                      const uint8_t* rec, const int8_t* qs, const uint16_t* d,
+                      int rows, int in, uint16_t* out, int ld, void* stream) {
+  if (rows <= 0 || in <= 0 || in % 256 || ld < in || (ld & 7) || fmt < 0 ||
+      fmt > DQ_RTN8 || ((fmt == DQ_SB6_5 || fmt == DQ_SB6_6 || fmt == DQ_SYM6) && !hb))
+    return RWKVQ_ERR_ARG;
+  return launch_wide<_Float16>(fmt, q, hb, rec, qs, d, rows, in,
+                               reinterpret_cast<_Float16*>(out), ld,
+                               (hipStream_t)stream);
 }
 
 }  // extern "C"

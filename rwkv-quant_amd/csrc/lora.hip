@@ -35,7 +35,7 @@ __device__ __forceinline__ float epi_apply(float v, int epi) {
   }
 }
 
-// One wave handles 8 rows of one branch.
+// One wave handles 4 (wide) or 8 (narrow) rows of one branch.
 // Wide rows (in = 64 * PER, PER in {32, 40}): the 64 lanes split each row,
 // lane owns PER columns; 4 rows are decoded together so their weight loads
 // are in flight at once, x is read once per (wave, input row).
@@ -45,52 +45,50 @@ __device__ __forceinline__ float epi_apply(float v, int epi) {
 constexpr int kMaxPer = 64;
 
 template <int PER>
-__device__ __forceinline__ void lora_wide(const LoraJob& jo, int N, int lw, int lane) {
-  // lane l owns fp16 pairs p = l + 64 q (q < PER / 2): consecutive lanes
-  // read consecutive dwords of the row (coalesced 256 B per instruction)
+__device__ __forceinline__ void lora_wide(const LoraJob& jo, int N, int lw,
+                                          int lane) {
+  // 4 rows per wave, all their weight loads in flight at once; lane l owns
+  // fp16 pairs p = l + 64 q (q < PER / 2), so consecutive lanes read
+  // consecutive dwords of a row (coalesced 256 B per instruction)
   constexpr int PW = PER / 2;
-  float res[2][8][4];                          // stores deferred to the end
+  float res[8][4];                             // stores deferred to the end
+  uint32_t wv[4][PW];
 #pragma unroll
-  for (int r0 = 0; r0 < 8; r0 += 4) {
-    uint32_t wv[4][PW];
+  for (int j = 0; j < 4; ++j) {
+    const int row = min(lw * 4 + j, jo.rows - 1);
+    const uint32_t* wr =
+        reinterpret_cast<const uint32_t*>(jo.W + (size_t)row * jo.in);
+#pragma unroll
+    for (int q = 0; q < PW; ++q) wv[j][q] = wr[lane + 64 * q];
+  }
+#pragma unroll
+  for (int n = 0; n < 8; ++n) {
+    if (n >= N) break;
+    const float2* xp =
+        reinterpret_cast<const float2*>(jo.x + (size_t)n * jo.x_ld);
+    uint32_t xh[PW];
+#pragma unroll
+    for (int q = 0; q < PW; ++q) {
+      const float2 f = xp[lane + 64 * q];
+      xh[q] = pack_h2(f.x, f.y);
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int row = min(lw * 8 + r0 + j, jo.rows - 1);
-      const uint32_t* wr =
-          reinterpret_cast<const uint32_t*>(jo.W + (size_t)row * jo.in);
+      float a = 0.f;
 #pragma unroll
-      for (int q = 0; q < PW; ++q) wv[j][q] = wr[lane + 64 * q];
-    }
-#pragma unroll
-    for (int n = 0; n < 8; ++n) {
-      if (n >= N) break;
-      const float2* xp =
-          reinterpret_cast<const float2*>(jo.x + (size_t)n * jo.x_ld);
-      uint32_t xh[PW];
-#pragma unroll
-      for (int q = 0; q < PW; ++q) {
-        const float2 f = xp[lane + 64 * q];
-        xh[q] = pack_h2(f.x, f.y);
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        float a = 0.f;
-#pragma unroll
-        for (int q = 0; q < PW; ++q) a = dot2(wv[j][q], xh[q], a);
-        res[r0 >> 2][n][j] = wave_sum_dpp(a);
-      }
+      for (int q = 0; q < PW; ++q) a = dot2(wv[j][q], xh[q], a);
+      res[n][j] = wave_sum_dpp(a);
     }
   }
-  if (lane < 8) {
+  if (lane < 4) {
 #pragma unroll
-    for (int rr = 0; rr < 8; ++rr) {
-      const int row = lw * 8 + rr;
-      if (rr != lane || row >= jo.rows) continue;
+    for (int j = 0; j < 4; ++j) {
+      const int row = lw * 4 + j;
+      if (j != lane || row >= jo.rows) continue;
 #pragma unroll
       for (int n = 0; n < 8; ++n)
         if (n < N)
-          jo.y[(size_t)n * jo.y_ld + row] =
-              epi_apply(res[rr >> 2][n][rr & 3], jo.epi);
+          jo.y[(size_t)n * jo.y_ld + row] = epi_apply(res[n][j], jo.epi);
     }
   }
 }
@@ -139,10 +137,14 @@ __device__ __forceinline__ void lora_narrow(const LoraJob& jo, int N, int lw, in
 __device__ __forceinline__ void lora_run(const LoraJob& jo, int N, int gw,
                                          int lane) {
   const int lw = gw - jo.wave0;
-  if (lw * 8 >= jo.rows) return;
-  if (jo.in == 64 * 32) lora_wide<32>(jo, N, lw, lane);
-  else if (jo.in == 64 * 40) lora_wide<40>(jo, N, lw, lane);
-  else lora_narrow(jo, N, lw, lane);
+  if (jo.in == 64 * 32 || jo.in == 64 * 40) {
+    if (lw * 4 >= jo.rows) return;
+    if (jo.in == 64 * 32) lora_wide<32>(jo, N, lw, lane);
+    else lora_wide<40>(jo, N, lw, lane);
+  } else {
+    if (lw * 8 >= jo.rows) return;
+    lora_narrow(jo, N, lw, lane);
+  }
 }
 
 __global__ void __launch_bounds__(256)
@@ -188,7 +190,7 @@ extern "C" int rwkvq_lora_gemv(int n_jobs, const void* const* W,
     j.rows = rows[q]; j.in = in[q]; j.x_ld = x_ld[q]; j.y_ld = y_ld[q];
     j.epi = epi[q];
     j.wave0 = waves;
-    waves += (rows[q] + 7) / 8;
+    waves += wide ? (rows[q] + 3) / 4 : (rows[q] + 7) / 8;
   }
   hipLaunchKernelGGL(lora_gemv_k, dim3((waves + 3) / 4), dim3(256), 0,
                      (hipStream_t)stream, J);

@@ -83,10 +83,24 @@ class _HipLinearBase:
         return torch.matmul(x2.half(), w.t()).float()
 
     def _dequant_w(self, dtype=torch.float16):
+        """Dense [OUT, IN]; float32 is bit-exact with the format's dequant,
+        float16 is exactly its one rounding (rwkvq_dequant_f16)."""
+        if dtype == torch.float16 and self._f16_args() is not None:
+            w = torch.empty((self.out_features, self.in_features),
+                            dtype=torch.float16, device=self.device)
+            fmt, q, hb, rec, qs, d = self._f16_args()
+            _lib.call("rwkvq_dequant_f16", fmt, _lib.ptr(q), _lib.ptr(hb),
+                      _lib.ptr(rec), _lib.ptr(qs), _lib.ptr(d),
+                      self.out_features, self.in_features, _lib.ptr(w),
+                      self.in_features, _lib.stream_handle())
+            return w
         w = torch.empty((self.out_features, self.in_features),
                         dtype=torch.float32, device=self.device)
         self._dequant_into(w)
         return w if dtype == torch.float32 else w.to(dtype)
+
+    def _f16_args(self):
+        return None
 
 
 class GwQuantLinear(_HipLinearBase):
@@ -120,6 +134,9 @@ class GwQuantLinear(_HipLinearBase):
                   _lib.ptr(x2), x_ld, _lib.ptr(y),
                   n if n is not None else x2.shape[0] // k, mode,
                   _lib.stream_handle())
+
+    def _f16_args(self):
+        return (self.bits - 4, self.nib, self.hb, self.rec, None, None)
 
     def _dequant_into(self, w):
         _lib.call("rwkvq_dequant_sb6_f32", _lib.ptr(self.nib),
@@ -180,6 +197,10 @@ class SymQuantLinear(_HipLinearBase):
                   _lib.ptr(y), n if n is not None else x2.shape[0] // k,
                   mode, _lib.stream_handle())
 
+    def _f16_args(self):
+        return (3 if self.bits == 6 else 4, self.codes, self.hb, None,
+                self.qs, self.d)
+
     def _dequant_into(self, w):
         _lib.call("rwkvq_dequant_sym_f32", _lib.ptr(self.codes),
                   _lib.ptr(self.hb), _lib.ptr(self.qs), _lib.ptr(self.d),
@@ -224,6 +245,11 @@ class QuantLinearV2(_HipLinearBase):
             # codes are 0 at outlier positions; add x[c] * value
             y.index_add_(1, self._out_rows,
                          x2[:, self._out_cols] * self._out_vals)
+
+    def _f16_args(self):
+        if self.has_outliers:
+            return None
+        return (5, self.codes, None, None, None, self.scale)
 
     def _dequant_into(self, w):
         _lib.call("rwkvq_dequant_rtn8_f32", _lib.ptr(self.codes),

@@ -445,11 +445,22 @@ class QuantRWKV7:
         return wk.xo.reshape(B, T, -1).clone(), out
 
     def forward_stateful(self, idx, states, last_only=False, tail_only=0):
-        """idx [B, T] -> (logits [B, T', V], new_states)."""
+        """idx [B, T] -> (logits [B, T', V], new_states).  With USE_GRAPH a
+        HIP graph is captured once per (B, T, last_only, tail_only) and
+        replayed (the analogue of the reference's compiled step, which
+        traces once per shape: reference quant_model.py:910-942)."""
         idx = self._idx(idx)
         B, T = idx.shape
-        wk = self._work_for(B * T)
+        if USE_GRAPH and T > 1:
+            return self._replay_seq(idx, states, last_only, tail_only)
         out = self._new_states(B)
+        logits = self._forward_into(idx, states, out, last_only, tail_only)
+        return logits.reshape(B, -1, self.vocab_size), out
+
+    def _forward_into(self, idx, states, out, last_only, tail_only,
+                      logits=None):
+        B, T = idx.shape
+        wk = self._work_for(B * T)
         self._body(idx, states, wk, out)
         xo = wk.xo.reshape(B, T, -1)
         if last_only and T > 1:
@@ -457,9 +468,65 @@ class QuantRWKV7:
         elif tail_only and T > tail_only:
             xo = xo[:, -tail_only:]
         xo = xo.reshape(-1, self.n_embd).contiguous()
-        logits = torch.empty(xo.shape[0], self.vocab_size, device=self.device)
+        if logits is None:
+            logits = torch.empty(xo.shape[0], self.vocab_size,
+                                 device=self.device)
         _apply(self.head, xo, logits, _lib.EPI_STORE)
-        return logits.reshape(B, -1, self.vocab_size), out
+        return logits
+
+    def _replay_seq(self, idx, states, last_only, tail_only):
+        B, T = idx.shape
+        key = (B, T, bool(last_only), int(tail_only))
+        g = self._graphs.get(key)
+        if g is None:
+            g = self._capture_seq(*key)
+            self._graphs[key] = g
+        g["idx"].copy_(idx)
+        self._load_states(g["in"], states)
+        g["graph"].replay()
+        new = [(s.clone(), t.clone(), c.clone()) for s, t, c in g["out"]]
+        return g["logits"].clone().reshape(B, -1, self.vocab_size), new
+
+    @staticmethod
+    def _load_states(dst, states):
+        for (si, ti, ci), (wi, tsi, csi) in zip(dst, states):
+            si.copy_(wi)
+            if tsi is None:
+                ti.zero_()
+            else:
+                ti.copy_(tsi)
+            if csi is None:
+                ci.zero_()
+            else:
+                ci.copy_(csi)
+
+    def _capture_seq(self, B, T, last_only, tail_only):
+        dev = self.device
+        idx = torch.zeros(B, T, dtype=torch.int64, device=dev)
+        st_in, st_out = self._new_states(B), self._new_states(B)
+        for s in st_in:
+            for t in s:
+                t.zero_()
+        rows = B if (last_only and T > 1) else (
+            B * tail_only if (tail_only and T > tail_only) else B * T)
+        logits = torch.empty(rows, self.vocab_size, device=dev)
+
+        def run():
+            self._forward_into(idx, st_in, st_out, last_only, tail_only,
+                               logits)
+
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            run()
+        torch.cuda.current_stream(dev).wait_stream(side)
+        torch.cuda.synchronize(dev)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            run()
+        torch.cuda.synchronize(dev)
+        return {"graph": graph, "idx": idx, "in": st_in, "out": st_out,
+                "logits": logits}
 
     def __call__(self, idx):
         idx = self._idx(idx)
@@ -481,16 +548,7 @@ class QuantRWKV7:
             self._graphs[B] = g
         g["idx"].copy_(idx)
         g["next"] = 0
-        for (si, ti, ci), (wi, tsi, csi) in zip(g["in"], states):
-            si.copy_(wi)
-            if tsi is None:
-                ti.zero_()
-            else:
-                ti.copy_(tsi)
-            if csi is None:
-                ci.zero_()
-            else:
-                ci.copy_(csi)
+        self._load_states(g["in"], states)
         g["graph"].replay()
         new = [(s.clone(), t.clone(), c.clone()) for s, t, c in g["out"]]
         return g["logits"].clone().reshape(B, 1, -1), new

@@ -51,6 +51,15 @@ def test_dequant_bit_exact(kind, bits, shape):
     _assert_same_bits(dev, ref)
 
 
+@pytest.mark.parametrize("kind,bits", FORMATS)
+def test_dequant_f16_is_one_rounding_of_f32(kind, bits):
+    w = _w(72, 2560, seed=13, degenerate=True, outliers=3)
+    lin = LIN[kind](qt_for(kind, bits, w))
+    w32 = lin._dequant_w(torch.float32)
+    w16 = lin._dequant_w(torch.float16)
+    assert torch.equal(w16, w32.half())
+
+
 def test_dequant_asym_bit_exact():
     w = weights(96, 2048, seed=5)
     qt = qt_for("asym", 6, w)

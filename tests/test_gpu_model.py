@@ -172,3 +172,21 @@ def test_fused_decode_core_equals_three_kernels(layer0):
     assert rel(st_a, st_b) < 1e-5
     assert rel(out_a, out_b) < 1e-5
     assert torch.equal(vf1, vf2)
+
+
+def test_graph_prefill_equals_eager(toy):
+    """forward_stateful replays a per-shape graph; it must equal the eager
+    launch sequence bit for bit, replay after replay."""
+    ck, orc, model = toy
+    idx = torch.from_numpy(np.random.default_rng(8).integers(0, 1024, (2, 9)))
+    qm.USE_GRAPH = False
+    try:
+        ref, st_ref = model.forward_stateful(idx, model.init_state(2))
+    finally:
+        qm.USE_GRAPH = True
+    for _ in range(3):
+        out, st = model.forward_stateful(idx, model.init_state(2))
+        assert torch.equal(out, ref)
+        for a, b in zip(st, st_ref):
+            for x, y in zip(a, b):
+                assert torch.equal(x, y)
