@@ -153,6 +153,7 @@ def gemv_set_bench(args, qts, dev):
     reps = max(1, args.steps // args.copies)
     for _ in range(max(1, args.warmup // args.copies)):
         set_graph.replay()
+    _mark()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
     t0, t1 = (torch.cuda.Event(enable_timing=True) for _ in range(2))
@@ -180,6 +181,52 @@ def gemv_set_bench(args, qts, dev):
     return ms_per_step, steps, kern
 
 
+MARK_KERNEL = "spin_kernel"
+
+
+def _mark():
+    """A ~1 us spin kernel launched just before a timed region, so that a
+    kernel trace of the run can be cut at it (--trace-summary)."""
+    import torch
+    torch.cuda._sleep(1000)
+
+
+def trace_summary(path, top=40):
+    """Per-kernel table of a rocprofv3 kernel_trace.csv, over the dispatches
+    after the last marker kernel (the last timed region of the run)."""
+    import csv
+    import re
+    rows = list(csv.DictReader(open(path)))
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    cut = max((i for i, r in enumerate(rows) if MARK_KERNEL in
+               r["Kernel_Name"]), default=-1)
+    rows = rows[cut + 1:]
+    agg = {}
+    for r in rows:
+        name = re.sub(r"\(.*", "", r["Kernel_Name"].replace(
+            "(anonymous namespace)::", "").replace("void ", ""))
+        key = (name[:72], r.get("Grid_Size", r.get("Grid_Size_X")),
+               r.get("Workgroup_Size", r.get("Workgroup_Size_X")))
+        d = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+        a = agg.setdefault(key, [0, 0, 1 << 62, 0])
+        a[0] += 1
+        a[1] += d
+        a[2] = min(a[2], d)
+        a[3] = max(a[3], d)
+    total = sum(a[1] for a in agg.values())
+    span = (int(rows[-1]["End_Timestamp"]) - int(rows[0]["Start_Timestamp"])
+            if rows else 0)
+    print(f"dispatches after the marker: {len(rows)}; kernel time "
+          f"{total / 1e3:.1f} us; span first start -> last end "
+          f"{span / 1e3:.1f} us")
+    print(f"{'kernel':72s} {'grid':>8s} {'wg':>4s} {'calls':>6s} "
+          f"{'avg_us':>8s} {'min_us':>8s} {'max_us':>8s} {'share':>6s}")
+    for (name, grid, wg), (n, tot, mn, mx) in sorted(
+            agg.items(), key=lambda kv: -kv[1][1])[:top]:
+        print(f"{name:72s} {grid:>8s} {wg:>4s} {n:6d} {tot / n / 1e3:8.2f} "
+              f"{mn / 1e3:8.2f} {mx / 1e3:8.2f} {100 * tot / total:5.1f}%")
+
+
 def decode_bench(preset, batches, n_tok, dev):
     """ms per decode step of the 1.5B-shaped model (graph replay, state
     carried between steps, fresh uniform-random token ids each step)."""
@@ -200,6 +247,7 @@ def decode_bench(preset, batches, n_tok, dev):
         for t in range(4):                     # warm-up + capture
             model.decode_replay(B, ids[t])
         model.reset_replay_state(B)
+        _mark()
         torch.cuda.synchronize()
         e0, e1 = (torch.cuda.Event(enable_timing=True) for _ in range(2))
         e0.record()
@@ -222,6 +270,7 @@ def prefill_bench(model, T, dev, reps=5):
     st = model.init_state(1)
     model.forward_stateful(idx, st)              # capture + warm-up
     gr = model._graphs[(1, T, False, 0)]
+    _mark()
     torch.cuda.synchronize()
     e0, e1 = (torch.cuda.Event(enable_timing=True) for _ in range(2))
     e0.record()
@@ -234,6 +283,65 @@ def prefill_bench(model, T, dev, reps=5):
     return {"T": T, "ms": round(ms, 3), "tok_s": round(T * 1e3 / ms, 1)}
 
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_head_rtn8_traffic.md")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the head GEMV, from the two rocprofv3 --pmc
+    passes (FETCH_SIZE, WRITE_SIZE) summarised in profiles/ -- counters are
+    not readable from inside a run, so the figure is the committed one.
+    Returns (bytes or None, source)."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":")[1]), os.path.relpath(
+                        TRAFFIC_FILE, ROOT)
+    except OSError:
+        pass
+    return None, None
+
+
+def pmc_pass(args, dev):
+    """Small eager workloads for rocprofv3 --pmc passes (one dispatch per
+    kernel launch, no graphs): 'set' = the 3-GEMV set, 'copy' = a plain
+    fp32 copy kernel of 256 MiB (the counter calibration)."""
+    import torch
+    if args.pmc_pass == "copy":
+        n = 64 << 20
+        src = torch.ones(n, device=dev)
+        dst = torch.empty(n, device=dev)
+        for _ in range(args.steps):
+            torch.mul(src, 1.0, out=dst)
+        torch.cuda.synchronize()
+        print(f"pmc copy pass: {args.steps} x {n * 4} B read + {n * 4} B "
+              f"written", flush=True)
+        return
+    from rwkv_quant.backends.hip.quant_linear import (QuantLinearV2,
+                                                      SymQuantLinear)
+    qts = build_set()
+    lins = {n: (QuantLinearV2(qt) if n == "head" else SymQuantLinear(qt))
+            for n, qt in qts.items()}
+    x = {n: torch.randn(1, qt.shape[1], device=dev) for n, qt in qts.items()}
+    y = {n: torch.empty(1, qt.shape[0], device=dev) for n, qt in qts.items()}
+    for _ in range(args.steps):
+        for n, lin in lins.items():
+            lin.gemv_into(x[n], y[n])
+    torch.cuda.synchronize()
+    per = algorithmic_bytes(qts)
+    print(f"pmc set pass: {args.steps} passes, algorithmic bytes per launch "
+          f"{per}", flush=True)
+
+
+def pp512(model, dev):
+    """pp512 with the projection FLOP rate (2 * 1.39e9 weight elements
+    of the 1.5B shape per token, head included)."""
+    pf = prefill_bench(model, 512, dev)
+    flop = 2 * 1_392_246_784 * 512
+    pf["tflop_s"] = round(flop / (pf["ms"] * 1e-3) / 1e12, 2)
+    return pf
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -244,22 +352,51 @@ def main():
     ap.add_argument("--no-model", action="store_true",
                     help="skip the 1.5B decode / pp512 measurements")
     ap.add_argument("--decode-tokens", type=int, default=128)
+    ap.add_argument("--only", choices=("decode", "prefill"), default=None,
+                    help="run one model workload alone (for a per-workload "
+                         "rocprofv3 profile); prints that section only")
+    ap.add_argument("--decode-batches", default="1,8",
+                    help="decode batch sizes for --only decode")
+    ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
+                    help="print the per-kernel table of a rocprofv3 kernel "
+                         "trace after its last marker kernel and exit")
+    ap.add_argument("--pmc-pass", choices=("set", "copy"), default=None,
+                    help="run a short eager workload for a rocprofv3 --pmc "
+                         "pass and exit (no JSON line)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for "
               f"--gpus {args.gpus}); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
+    if args.trace_summary:
+        trace_summary(args.trace_summary)
+        return
+
     import torch
     from rwkv_quant.backends.hip import _lib
     _lib.load()
     dev = torch.device("cuda:0")
+    if args.pmc_pass:
+        pmc_pass(args, dev)
+        return
+    if args.only == "decode":
+        bs = tuple(int(b) for b in args.decode_batches.split(","))
+        _, dec = decode_bench("compression", bs, args.decode_tokens, dev)
+        print(json.dumps({"decode_1p5b_compression": dec}), flush=True)
+        return
+    if args.only == "prefill":
+        model, _ = decode_bench("reduction", (), 0, dev)
+        print(json.dumps({"pp512_1p5b_reduction":
+                          pp512(model, dev)}), flush=True)
+        return
     qts = build_set()
     per = algorithmic_bytes(qts)
     set_bytes = sum(per.values())
     ms_per_step, steps, kern = gemv_set_bench(args, qts, dev)
     achieved = per["head"] / (kern["head"] * 1e-3) / 1e9
     value = set_bytes / (ms_per_step * 1e-3) / 1e9
+    traffic, traffic_src = measured_traffic()
 
     out = {
         "metric": "quant GEMV GB/s (% HBM peak)",
@@ -282,7 +419,8 @@ def main():
         "roofline": {"bound": "hbm", "kernel": "gemv_kernel<F_RTN8> (head)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None,
+                     "traffic": traffic,
+                     "traffic_source": traffic_src,
                      "launch_us": round(kern["head"] * 1e3, 3),
                      "bytes_per_launch": per["head"]},
         "cpu_baseline": None,
@@ -295,10 +433,7 @@ def main():
         torch.cuda.empty_cache()
         model, dec_r = decode_bench("reduction", (1,), 32, dev)
         out["decode_1p5b_reduction"] = dec_r
-        pf = prefill_bench(model, 512, dev)
-        flop = 2 * 1_392_246_784 * 512
-        pf["tflop_s"] = round(flop / (pf["ms"] * 1e-3) / 1e12, 2)
-        out["pp512_1p5b_reduction"] = pf
+        out["pp512_1p5b_reduction"] = pp512(model, dev)
         del model
         torch.cuda.empty_cache()
     if not args.no_cpu:

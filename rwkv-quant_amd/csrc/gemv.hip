@@ -194,7 +194,11 @@ gemv_kernel(GemvArgs a) {
   // matrix) so the compiler can count them and wait only for the batch it
   // consumes.
   const int nrows = min(a.rpw, a.rows - row_base);   // rows of this wave
-  const int last = a.rows - 1;
+  // loads past the wave's own rows are clamped to its last row (an L2 hit
+  // of data it has just read) rather than to the matrix's last row: the
+  // rows after them belong to another wave, possibly on another XCD, and
+  // reading them there costs a second HBM fetch
+  const int last = max(min(row_base + a.rpw, a.rows) - 1, 0);
   Raw cur[RS], nxt[RS];
 #pragma unroll
   for (int j = 0; j < RS; ++j)
