@@ -80,6 +80,36 @@ int rwkvq_gemv_rtn8(const int8_t* codes, const uint16_t* scale, int rows,
                     int in, int out_per, const float* x, long x_ld, float* y,
                     int n_cols, int epilogue, void* stream);
 
+/* ------------------------------------------------------ prefill GEMM
+ * y[t, :] = epilogue(x[t] @ W^T) for t < M tokens, on the matrix cores
+ * (v_mfma_f32_32x32x16_f16), W decoded from the same device layouts as the
+ * GEMV entry points; same arguments as rwkvq_gemv_* with M in place of
+ * n_cols.  Operands are fp16 exactly as the reference's prefill uses them
+ * (x rounded once; W = the format's dequant rounded once to fp16; rtn8
+ * multiplies the fp32 sum of x * code by its row scale), fp32 accumulate,
+ * fp32 out.  Output rows per input segment (out_per) must be a multiple of
+ * 128.  No dense copy of W is made.
+ *
+ * Replaces the reference's prefill path of the same linears, a dense fp16
+ * dequant followed by an fp16 matmul:
+ *   GwQuantLinear.__call__ / _dequant_w + mx.matmul
+ *       (rwkv_quant/backends/metal/quant_linear_gw.py:821-849)
+ *   SymQuantLinear.__call__ GEMM branch
+ *       (rwkv_quant/backends/metal/quant_linear_sym.py:433-484)
+ *   QuantLinearV2.__call__ GEMM branch
+ *       (rwkv_quant/backends/metal/quant_linear_v2.py:322-351)
+ */
+int rwkvq_gemm_sb6(const uint8_t* nib, const uint32_t* hb, const uint8_t* rec,
+                   int bits, int rows, int in, int out_per, const float* x,
+                   long x_ld, float* y, int M, int epilogue, void* stream);
+int rwkvq_gemm_sym(const uint8_t* codes, const uint32_t* hb, const int8_t* qs,
+                   const uint16_t* d, int bits, int rows, int in, int out_per,
+                   const float* x, long x_ld, float* y, int M, int epilogue,
+                   void* stream);
+int rwkvq_gemm_rtn8(const int8_t* codes, const uint16_t* scale, int rows,
+                    int in, int out_per, const float* x, long x_ld, float* y,
+                    int M, int epilogue, void* stream);
+
 /* ------------------------------------------------------ dequant to fp32
  * Bit-exact with the format's dequant formula: w = q * s + m with
  * s = max(f32(f16(qs * d)), 1e-8), m = f32(f16(qm * dm)) (sb6);

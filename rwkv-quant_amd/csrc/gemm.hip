@@ -1,0 +1,364 @@
+// Prefill GEMM with the dequantization fused into the operand load, on the
+// gfx950 matrix cores (v_mfma_f32_32x32x16_f16).
+//
+//   y[t, n] = epi( sum_k x[t, seg(n) * K + k] * W[n, k] )
+//
+// x is fp32 [M, x_ld] (tokens), W one of the packed `.rwkvq` device layouts,
+// y fp32 [M, N].  The reference runs this step as a dense fp16 dequant of W
+// followed by an fp16 matmul with fp32 output
+// (reference: rwkv_quant/backends/metal/quant_linear_gw.py:821-849,
+//             rwkv_quant/backends/metal/quant_linear_sym.py:433-484,
+//             rwkv_quant/backends/metal/quant_linear_v2.py:322-351);
+// here no dense copy of W exists: each lane decodes its codes into the fp16
+// weight the reference's dequant would give and feeds them straight to the
+// MFMA as the A operand, so W is read from HBM once per token tile.
+//
+// Roles in the 32x32x16 MFMA: A = W (row i <-> output n), B = x^T (column
+// j <-> token t).  Lane l holds A[i = l % 32][k = 8 * (l / 32) + e] and
+// B[k = 8 * (l / 32) + e][j = l % 32], e = 0..7; D[i][j] lands in lane
+// l = j + 32 * ((i / 4) % 2), register v = 4 * (i / 8) + i % 4.
+//
+// The k order inside a 32-column quant group is the decoder's pair order
+// (x_cols): x is written to LDS in that same order, so both operands walk k
+// identically and the sum is the plain dot product.
+//
+// Tiling: a workgroup of 4 waves covers BN = 4 * 32 * WN output rows and
+// BM = 32 * WM tokens.  A wave owns 32 * WN rows (its W fragments stay in
+// registers, nothing of W goes through LDS) and all BM tokens.  The K loop
+// takes 128 columns per step: lane half h decodes groups 2h and 2h+1 of
+// the step; x of the step (BM x 128, fp16, pair order) is staged in LDS,
+// double-buffered, one barrier per step.  Weights and x of step c + 1 are
+// loaded into registers before the MFMAs of step c.
+//
+// Weight values (fp16, exactly as the format's dequant rounded once):
+//   sb6   w = fma(q, f16(s), f16(m))   (s = max(f32(f16(qs*d)), 1e-8))
+//   sym   w = q * f16(qs * d)
+//   rtn8  w = q, the fp32 row scale multiplies the fp32 sum
+#include "qfmt.h"
+#include "rwkvq_hip.h"
+
+using namespace rwkvq;
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+namespace {
+
+struct GemmArgs {
+  const uint8_t* q;
+  const uint32_t* hb;
+  const uint8_t* rec;
+  const int8_t* qs;
+  const uint16_t* d;
+  const float* x;        // x[t * x_ld + seg * K + k]
+  float* y;              // y[t * N + n]
+  long x_ld;
+  int M, N, in, out_per, mode;
+};
+
+constexpr int kStepK = 128;                 // columns per K step
+constexpr int kRowH = kStepK + 8;           // LDS row stride in halves
+
+__device__ __forceinline__ uint32_t h2_bits(h2_t v) {
+  return __builtin_bit_cast(uint32_t, v);
+}
+__device__ __forceinline__ h2_t as_h2(uint32_t u) {
+  return __builtin_bit_cast(h2_t, u);
+}
+
+// fp16 weights of one (row, group) in the decoder's pair order.
+template <int FMT>
+__device__ __forceinline__ void dequant_group(const Raw& r, int kb,
+                                              uint32_t w[16]) {
+  decode_raw<FMT>(r, w);
+  if (FMT <= F_SB6_6) {
+    const uint32_t rr[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
+    const int qs_word = (6 * kb) >> 5, qs_sh = (6 * kb) & 31;
+    const int qm_word = (48 + 6 * kb) >> 5, qm_sh = (48 + 6 * kb) & 31;
+    uint32_t lo = qs_word == 0 ? rr[0] : rr[1];
+    uint32_t hi = qs_word == 0 ? rr[1] : rr[2];
+    const uint32_t qsv = __builtin_amdgcn_alignbit(hi, lo, (uint32_t)qs_sh) & 63u;
+    lo = qm_word == 1 ? rr[1] : rr[2];
+    hi = qm_word == 1 ? rr[2] : rr[3];
+    const uint32_t qmv = __builtin_amdgcn_alignbit(hi, lo, (uint32_t)qm_sh) & 63u;
+    const float d = f16_bits_to_f32(rr[3] & 0xFFFFu);
+    const float dm = f16_bits_to_f32(rr[3] >> 16);
+    const _Float16 s = (_Float16)fmaxf(f16_round((float)qsv * d), 1e-8f);
+    const _Float16 m = (_Float16)((float)((int)qmv - 31) * dm);
+    const h2_t s2 = {s, s}, m2 = {m, m}, bias = {(_Float16)1024.f, (_Float16)1024.f};
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const h2_t q = as_h2(w[i]) - bias;                      // exact
+      w[i] = h2_bits(__builtin_elementwise_fma(q, s2, m2));  // one rounding
+    }
+  } else if (FMT == F_SYM6 || FMT == F_SYM8) {
+    const float d = f16_bits_to_f32(r.s >> 16);
+    const _Float16 sa = (_Float16)((float)(int8_t)(r.s & 0xFFu) * d);
+    const _Float16 sb = (_Float16)((float)(int8_t)((r.s >> 8) & 0xFFu) * d);
+    const _Float16 mb = (_Float16)magic_bias<FMT>();
+    const h2_t bias = {mb, mb}, a2 = {sa, sa}, b2 = {sb, sb};
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const h2_t q = as_h2(w[i]) - bias;                      // exact
+      w[i] = h2_bits(q * (i < 8 ? a2 : b2));                  // one rounding
+    }
+  } else {
+    const h2_t bias = {(_Float16)1152.f, (_Float16)1152.f};
+#pragma unroll
+    for (int i = 0; i < 16; ++i) w[i] = h2_bits(as_h2(w[i]) - bias);
+  }
+}
+
+// Columns (within a group) of the two float4s that sub-step s of the pair
+// order reads: pairs 4s..4s+3.
+template <int FMT>
+__device__ __forceinline__ void step_cols(int s, int& ca, int& cb) {
+  if (FMT <= F_SB6_6) { ca = 4 * s; cb = 4 * s + 16; }
+  else if (FMT == F_SYM6) { ca = (s < 2 ? 4 * s : 4 * s + 8); cb = ca + 8; }
+  else { ca = 8 * s; cb = 8 * s + 4; }
+}
+
+// 8 x values of one (token, group, sub-step) -> 4 fp16 pairs in pair order.
+template <int FMT>
+__device__ __forceinline__ uint4 x_pairs(float4 A, float4 B) {
+  if (FMT == F_SYM8 || FMT == F_RTN8)      // pairs (2i, 2i+1)
+    return make_uint4(pack_h2(A.x, A.y), pack_h2(A.z, A.w),
+                      pack_h2(B.x, B.y), pack_h2(B.z, B.w));
+  return make_uint4(pack_h2(A.x, B.x), pack_h2(A.y, B.y),   // (c0, c1)
+                    pack_h2(A.z, B.z), pack_h2(A.w, B.w));
+}
+
+template <int FMT, int WN, int WM>
+__global__ void __launch_bounds__(256)
+gemm_kernel(GemmArgs a) {
+  constexpr int BM = 32 * WM;
+  constexpr int BN = 128 * WN;
+  constexpr int XI = BM * 16 / 256;          // staging items per thread
+  __shared__ __attribute__((aligned(16))) _Float16 sx[2][BM * kRowH];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane & 31, h = lane >> 5;
+  const int n0 = blockIdx.x * BN;
+  const int m0 = blockIdx.y * BM;
+  const int seg = n0 / a.out_per;
+  const int ng = a.in >> 5, nsb = a.in >> 8;
+  const int nsteps = a.in / kStepK;
+  const float* xb = a.x + (size_t)seg * a.in;
+
+  // ---- x staging: item = (token, group of the step, sub-step)
+  float4 xa[XI], xbv[XI];
+  auto load_x = [&](int c) {
+#pragma unroll
+    for (int p = 0; p < XI; ++p) {
+      const int it = threadIdx.x + 256 * p;
+      const int t = min(m0 + (it >> 4), a.M - 1);
+      const int gq = (it >> 2) & 3, s = it & 3;
+      int ca, cb;
+      step_cols<FMT>(s, ca, cb);
+      const float* src = xb + (size_t)t * a.x_ld + c * kStepK + gq * 32;
+      xa[p] = *reinterpret_cast<const float4*>(src + ca);
+      xbv[p] = *reinterpret_cast<const float4*>(src + cb);
+    }
+  };
+  auto store_x = [&](int buf) {
+#pragma unroll
+    for (int p = 0; p < XI; ++p) {
+      const int it = threadIdx.x + 256 * p;
+      const int tl = it >> 4, gq = (it >> 2) & 3, s = it & 3;
+      *reinterpret_cast<uint4*>(&sx[buf][tl * kRowH + gq * 32 + s * 8]) =
+          x_pairs<FMT>(xa[p], xbv[p]);
+    }
+  };
+
+  // ---- weights: WN rows x 2 groups per lane per step
+  int rows[WN];
+#pragma unroll
+  for (int ni = 0; ni < WN; ++ni)
+    rows[ni] = n0 + wave * 32 * WN + ni * 32 + r;
+  Raw cur[WN][2], nxt[WN][2];
+  auto load_w = [&](int c, Raw (&dst)[WN][2]) {
+#pragma unroll
+    for (int ni = 0; ni < WN; ++ni)
+#pragma unroll
+      for (int gi = 0; gi < 2; ++gi)
+        load_raw<FMT>(a, rows[ni], ng, nsb, c * 4 + 2 * h + gi, dst[ni][gi]);
+  };
+
+  f32x16_t acc[WM][WN];
+#pragma unroll
+  for (int mi = 0; mi < WM; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < WN; ++ni)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[mi][ni][v] = 0.f;
+
+  load_w(0, cur);
+  load_x(0);
+  store_x(0);
+  __syncthreads();
+
+  for (int c = 0; c < nsteps; ++c) {
+    const int cn = min(c + 1, nsteps - 1);     // clamped: loads stay in W / x
+    load_w(cn, nxt);
+    load_x(cn);
+    const _Float16* xs = sx[c & 1];
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi) {
+      uint32_t w[WN][16];
+      const int kb = (c * 4 + 2 * h + gi) & 7;   // group within superblock
+#pragma unroll
+      for (int ni = 0; ni < WN; ++ni) dequant_group<FMT>(cur[ni][gi], kb, w[ni]);
+#pragma unroll
+      for (int ss = 0; ss < 4; ++ss) {
+        half8_t bx[WM];
+#pragma unroll
+        for (int mi = 0; mi < WM; ++mi)
+          bx[mi] = *reinterpret_cast<const half8_t*>(
+              xs + (mi * 32 + r) * kRowH + (2 * h + gi) * 32 + ss * 8);
+#pragma unroll
+        for (int ni = 0; ni < WN; ++ni) {
+          const uint4 wa = make_uint4(w[ni][4 * ss], w[ni][4 * ss + 1],
+                                      w[ni][4 * ss + 2], w[ni][4 * ss + 3]);
+          const half8_t av = __builtin_bit_cast(half8_t, wa);
+#pragma unroll
+          for (int mi = 0; mi < WM; ++mi)
+            acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                av, bx[mi], acc[mi][ni], 0, 0, 0);
+        }
+      }
+    }
+    store_x((c + 1) & 1);
+    __syncthreads();
+#pragma unroll
+    for (int ni = 0; ni < WN; ++ni)
+#pragma unroll
+      for (int gi = 0; gi < 2; ++gi) cur[ni][gi] = nxt[ni][gi];
+  }
+
+  // ---- epilogue: lane holds tokens m0 + 32 mi + r, rows 4 at a time
+#pragma unroll
+  for (int mi = 0; mi < WM; ++mi) {
+    const int t = m0 + mi * 32 + r;
+    if (t >= a.M) continue;
+    float* yrow = a.y + (size_t)t * a.N;
+#pragma unroll
+    for (int ni = 0; ni < WN; ++ni)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int n = n0 + wave * 32 * WN + ni * 32 + 8 * q + 4 * h;
+        float4 v = make_float4(acc[mi][ni][4 * q], acc[mi][ni][4 * q + 1],
+                               acc[mi][ni][4 * q + 2], acc[mi][ni][4 * q + 3]);
+        if (FMT == F_RTN8) {
+          const uint2 sc = *reinterpret_cast<const uint2*>(a.d + n);
+          v.x *= f16_bits_to_f32(sc.x & 0xFFFFu);
+          v.y *= f16_bits_to_f32(sc.x >> 16);
+          v.z *= f16_bits_to_f32(sc.y & 0xFFFFu);
+          v.w *= f16_bits_to_f32(sc.y >> 16);
+        }
+        float4* yp = reinterpret_cast<float4*>(yrow + n);
+        switch (a.mode) {
+          case RWKVQ_EPI_ADD: {
+            const float4 o = *yp;
+            v.x += o.x; v.y += o.y; v.z += o.z; v.w += o.w;
+            break;
+          }
+          case RWKVQ_EPI_RELU2:
+            v.x = v.x > 0.f ? v.x * v.x : 0.f; v.y = v.y > 0.f ? v.y * v.y : 0.f;
+            v.z = v.z > 0.f ? v.z * v.z : 0.f; v.w = v.w > 0.f ? v.w * v.w : 0.f;
+            break;
+          case RWKVQ_EPI_TANH:
+            v.x = tanhf(v.x); v.y = tanhf(v.y); v.z = tanhf(v.z); v.w = tanhf(v.w);
+            break;
+          case RWKVQ_EPI_SIGMOID:
+            v.x = 1.f / (1.f + __expf(-v.x)); v.y = 1.f / (1.f + __expf(-v.y));
+            v.z = 1.f / (1.f + __expf(-v.z)); v.w = 1.f / (1.f + __expf(-v.w));
+            break;
+          default: break;
+        }
+        *yp = v;
+      }
+  }
+}
+
+template <int FMT, int WN, int WM>
+int launch_tile(const GemmArgs& a, hipStream_t s) {
+  dim3 grid(a.N / (128 * WN), (a.M + 32 * WM - 1) / (32 * WM));
+  hipLaunchKernelGGL((gemm_kernel<FMT, WN, WM>), grid, dim3(256), 0, s, a);
+  return hipGetLastError() == hipSuccess ? RWKVQ_OK : RWKVQ_ERR_LAUNCH;
+}
+
+// Largest tile that still gives >= 256 workgroups (one per CU); N tiles of
+// 256 rows need out_per % 256 == 0.
+template <int FMT>
+int launch_gemm(const GemmArgs& a, hipStream_t s) {
+  auto wgs = [&](int bn, int bm) {
+    return (long)(a.N / bn) * ((a.M + bm - 1) / bm);
+  };
+  const bool wide = a.out_per % 256 == 0;
+  if (wide && wgs(256, 128) >= 256) return launch_tile<FMT, 2, 4>(a, s);
+  if (wide && wgs(256, 64) >= 256) return launch_tile<FMT, 2, 2>(a, s);
+  if (wgs(128, 64) >= 256) return launch_tile<FMT, 1, 2>(a, s);
+  return launch_tile<FMT, 1, 1>(a, s);
+}
+
+int check_gemm(int rows, int in, int out_per, int M, long x_ld, int mode) {
+  if (rows <= 0 || in <= 0 || M <= 0 || out_per <= 0) return RWKVQ_ERR_ARG;
+  if (in % 256) return RWKVQ_ERR_ARG;
+  if (rows % out_per || out_per % 128) return RWKVQ_ERR_ARG;
+  if (x_ld < (long)(rows / out_per) * in) return RWKVQ_ERR_ARG;
+  if (mode < 0 || mode > RWKVQ_EPI_SIGMOID) return RWKVQ_ERR_ARG;
+  return RWKVQ_OK;
+}
+
+GemmArgs make_args(int rows, int in, int out_per, const float* x, long x_ld,
+                   float* y, int M, int mode) {
+  GemmArgs a{};
+  a.x = x; a.y = y; a.M = M; a.N = rows; a.in = in; a.out_per = out_per;
+  a.mode = mode;
+  a.x_ld = x_ld > 0 ? x_ld : (long)(rows / out_per) * in;
+  return a;
+}
+
+}  // namespace
+
+extern "C" {
+
+int rwkvq_gemm_sb6(const uint8_t* nib, const uint32_t* hb, const uint8_t* rec,
+                   int bits, int rows, int in, int out_per, const float* x,
+                   long x_ld, float* y, int M, int mode, void* stream) {
+  GemmArgs a = make_args(rows, in, out_per, x, x_ld, y, M, mode);
+  int st = check_gemm(rows, in, out_per, M, a.x_ld, mode);
+  if (st) return st;
+  if (bits < 4 || bits > 6 || (bits > 4 && !hb)) return RWKVQ_ERR_ARG;
+  a.q = nib; a.hb = hb; a.rec = rec;
+  hipStream_t s = (hipStream_t)stream;
+  if (bits == 4) return launch_gemm<F_SB6_4>(a, s);
+  if (bits == 5) return launch_gemm<F_SB6_5>(a, s);
+  return launch_gemm<F_SB6_6>(a, s);
+}
+
+int rwkvq_gemm_sym(const uint8_t* codes, const uint32_t* hb, const int8_t* qs,
+                   const uint16_t* d, int bits, int rows, int in, int out_per,
+                   const float* x, long x_ld, float* y, int M, int mode,
+                   void* stream) {
+  GemmArgs a = make_args(rows, in, out_per, x, x_ld, y, M, mode);
+  int st = check_gemm(rows, in, out_per, M, a.x_ld, mode);
+  if (st) return st;
+  if ((bits != 6 && bits != 8) || (bits == 6 && !hb)) return RWKVQ_ERR_ARG;
+  a.q = codes; a.hb = hb; a.qs = qs; a.d = d;
+  hipStream_t s = (hipStream_t)stream;
+  return bits == 6 ? launch_gemm<F_SYM6>(a, s) : launch_gemm<F_SYM8>(a, s);
+}
+
+int rwkvq_gemm_rtn8(const int8_t* codes, const uint16_t* scale, int rows,
+                    int in, int out_per, const float* x, long x_ld, float* y,
+                    int M, int mode, void* stream) {
+  GemmArgs a = make_args(rows, in, out_per, x, x_ld, y, M, mode);
+  int st = check_gemm(rows, in, out_per, M, a.x_ld, mode);
+  if (st) return st;
+  a.q = reinterpret_cast<const uint8_t*>(codes); a.d = scale;
+  return launch_gemm<F_RTN8>(a, (hipStream_t)stream);
+}
+
+}  // extern "C"

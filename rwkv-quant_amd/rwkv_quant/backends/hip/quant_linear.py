@@ -15,8 +15,8 @@ Same contract as the reference Metal classes
                                matrices in one launch
 
 Batches of up to GEMM_MIN_BATCH_NB - 1 rows take the GEMV kernel (which
-reads each weight once per 4 rows); larger batches (prefill) take the GEMM
-path.  Every path runs a HIP kernel of librwkvq_hip; nothing here computes
+reads each weight once per 8 rows); larger batches (prefill) take the MFMA
+GEMM with the dequantization fused into its operand load.  Every path runs a HIP kernel of librwkvq_hip; nothing here computes
 on the CPU.
 """
 import numpy as np
@@ -26,7 +26,7 @@ from . import _lib
 from .repack import rtn8_device, sb6_device, sym_device
 
 GEMM_MIN_BATCH_NB = 128          # reference: quant_linear_gw.py:153
-NB_CHUNK = 4                     # rows per GEMV launch (kernel-internal)
+GEMM_ROW_TILE = 128              # output rows per MFMA GEMM tile
 
 
 def _np(t):
@@ -54,31 +54,79 @@ class _HipLinearBase:
     in_features: int
     device: torch.device
 
+    def _kargs(self):
+        """(entry-point suffix, leading arguments) of this format's GEMV /
+        GEMM entry points; both take the same argument list."""
+        raise NotImplementedError
+
+    def _run(self, kind, x2, y, out_per=None, mode=_lib.EPI_STORE, n=None,
+             x_ld=0):
+        k = 1 if out_per is None else self.out_features // out_per
+        suffix, lead = self._kargs()
+        _lib.call(f"rwkvq_{kind}_{suffix}", *lead, self.out_features,
+                  self.in_features, out_per or self.out_features,
+                  _lib.ptr(x2), x_ld, _lib.ptr(y),
+                  n if n is not None else x2.shape[0] // k, mode,
+                  _lib.stream_handle())
+
     def _gemv(self, x2, y, out_per=None, mode=_lib.EPI_STORE, n=None,
               x_ld=0):
-        raise NotImplementedError
+        self._run("gemv", x2, y, out_per, mode, n, x_ld)
+
+    def gemm_ok(self, out_per=None):
+        """The MFMA GEMM tiles output rows by 128 per input segment."""
+        return (out_per or self.out_features) % GEMM_ROW_TILE == 0
+
+    def _apply(self, x2, y, out_per=None, mode=_lib.EPI_STORE, n=None,
+               x_ld=0):
+        rows = n if n is not None else x2.shape[0]
+        if rows < GEMM_MIN_BATCH_NB:
+            self._gemv(x2, y, out_per, mode, n, x_ld)
+        elif self.gemm_ok(out_per):
+            self._run("gemm", x2, y, out_per, mode, n, x_ld)
+        else:
+            if out_per:
+                raise NotImplementedError("segmented input off the MFMA tiles")
+            if x_ld:
+                x2 = torch.as_strided(x2, (rows, self.in_features), (x_ld, 1))
+            out = self._gemm_dense(x2.contiguous(), _lib.EPI_STORE)
+            if mode == _lib.EPI_STORE:
+                y.copy_(out)
+            elif mode == _lib.EPI_ADD:
+                y.add_(out)
+            elif mode == _lib.EPI_RELU2:
+                y.copy_(torch.relu(out))
+                y.mul_(y)
+            else:
+                raise NotImplementedError(mode)
 
     def __call__(self, x, mode=_lib.EPI_STORE):
         lead, x2 = _flat_x(x, self.in_features)
         n = x2.shape[0]
-        if n >= GEMM_MIN_BATCH_NB and mode == _lib.EPI_STORE:
-            y = self._gemm(x2)
-        else:
-            y = torch.empty((n, self.out_features), dtype=torch.float32,
-                            device=x2.device)
-            self._gemv(x2, y, mode=mode)
+        y = torch.empty((n, self.out_features), dtype=torch.float32,
+                        device=x2.device)
+        self._apply(x2, y, mode=mode)
         return y.reshape(*lead, self.out_features)
 
     def gemv_into(self, x2, y, mode=_lib.EPI_STORE, n=None, x_ld=0):
-        """y [N, OUT] (preallocated) <- epi(x2 [N, IN] @ W^T).  With x_ld,
-        row n of the input starts at element n * x_ld of x2 (a strided
-        view); n is then the number of rows."""
+        """y [N, OUT] (preallocated) <- epi(x2 [N, IN] @ W^T) with the GEMV
+        kernel.  With x_ld, row n of the input starts at element n * x_ld of
+        x2 (a strided view); n is then the number of rows."""
         self._gemv(x2, y, mode=mode, n=n, x_ld=x_ld)
         return y
 
-    def _gemm(self, x2):
-        # prefill: dense fp16 weights from the bit-exact dequant kernel,
-        # fp16 GEMM with fp32 output (reference: quant_linear_gw.py:846-849)
+    def apply_into(self, x2, y, mode=_lib.EPI_STORE, n=None, x_ld=0):
+        """As gemv_into, with the kernel chosen by the row count: GEMV below
+        GEMM_MIN_BATCH_NB rows, the MFMA GEMM from there on."""
+        self._apply(x2, y, mode=mode, n=n, x_ld=x_ld)
+        return y
+
+    def _gemm_dense(self, x2, mode):
+        # shapes the MFMA tiles do not cover: dense fp16 weights from the
+        # dequant kernel and an fp16 matmul with fp32 output, the
+        # reference's own prefill path (reference: quant_linear_gw.py:846-849)
+        if mode != _lib.EPI_STORE:
+            raise NotImplementedError("dense GEMM path: store epilogue only")
         w = self._dequant_w(torch.float16)
         return torch.matmul(x2.half(), w.t()).float()
 
@@ -125,15 +173,9 @@ class GwQuantLinear(_HipLinearBase):
             else None
         self.rec = _dev(lay["rec"], self.device)
 
-    def _gemv(self, x2, y, out_per=None, mode=_lib.EPI_STORE, n=None,
-              x_ld=0):
-        k = 1 if out_per is None else self.out_features // out_per
-        _lib.call("rwkvq_gemv_sb6", _lib.ptr(self.nib), _lib.ptr(self.hb),
-                  _lib.ptr(self.rec), self.bits, self.out_features,
-                  self.in_features, out_per or self.out_features,
-                  _lib.ptr(x2), x_ld, _lib.ptr(y),
-                  n if n is not None else x2.shape[0] // k, mode,
-                  _lib.stream_handle())
+    def _kargs(self):
+        return "sb6", (_lib.ptr(self.nib), _lib.ptr(self.hb),
+                       _lib.ptr(self.rec), self.bits)
 
     def _f16_args(self):
         return (self.bits - 4, self.nib, self.hb, self.rec, None, None)
@@ -187,15 +229,9 @@ class SymQuantLinear(_HipLinearBase):
                 and self.in_features == other.in_features
                 and self.out_features == other.out_features)
 
-    def _gemv(self, x2, y, out_per=None, mode=_lib.EPI_STORE, n=None,
-              x_ld=0):
-        k = 1 if out_per is None else self.out_features // out_per
-        _lib.call("rwkvq_gemv_sym", _lib.ptr(self.codes), _lib.ptr(self.hb),
-                  _lib.ptr(self.qs), _lib.ptr(self.d), self.bits,
-                  self.out_features, self.in_features,
-                  out_per or self.out_features, _lib.ptr(x2), x_ld,
-                  _lib.ptr(y), n if n is not None else x2.shape[0] // k,
-                  mode, _lib.stream_handle())
+    def _kargs(self):
+        return "sym", (_lib.ptr(self.codes), _lib.ptr(self.hb),
+                       _lib.ptr(self.qs), _lib.ptr(self.d), self.bits)
 
     def _f16_args(self):
         return (3 if self.bits == 6 else 4, self.codes, self.hb, None,
@@ -231,18 +267,18 @@ class QuantLinearV2(_HipLinearBase):
             self._out_cols = oi[:, 1].to(self.device)
             self._out_vals = qt.outlier_values.float().to(self.device)
 
-    def _gemv(self, x2, y, out_per=None, mode=_lib.EPI_STORE, n=None,
-              x_ld=0):
-        k = 1 if out_per is None else self.out_features // out_per
-        if self.has_outliers and (mode != _lib.EPI_STORE or x_ld):
+    def _kargs(self):
+        return "rtn8", (_lib.ptr(self.codes), _lib.ptr(self.scale))
+
+    def _run(self, kind, x2, y, out_per=None, mode=_lib.EPI_STORE, n=None,
+             x_ld=0):
+        if self.has_outliers and (mode not in (_lib.EPI_STORE, _lib.EPI_ADD)
+                                  or x_ld or out_per):
             raise NotImplementedError("outliers with a fused epilogue")
-        _lib.call("rwkvq_gemv_rtn8", _lib.ptr(self.codes),
-                  _lib.ptr(self.scale), self.out_features, self.in_features,
-                  out_per or self.out_features, _lib.ptr(x2), x_ld,
-                  _lib.ptr(y), n if n is not None else x2.shape[0] // k,
-                  mode, _lib.stream_handle())
+        super()._run(kind, x2, y, out_per, mode, n, x_ld)
         if self.has_outliers:
-            # codes are 0 at outlier positions; add x[c] * value
+            # codes are 0 at outlier positions; add x[c] * value (linear, so
+            # also right after an accumulate epilogue)
             y.index_add_(1, self._out_rows,
                          x2[:, self._out_cols] * self._out_vals)
 
@@ -279,13 +315,20 @@ class _FusedBase:
                         x_ld=x_ld)
         return y
 
+    def apply_into(self, x, y, n, x_ld, mode=_lib.EPI_STORE):
+        """As gemv_into, GEMV below GEMM_MIN_BATCH_NB rows, MFMA GEMM from
+        there on."""
+        self._cat._apply(x, y, out_per=self.out_per, mode=mode, n=n,
+                         x_ld=x_ld)
+        return y
+
     def __call__(self, xstack, mode=_lib.EPI_STORE):
         lead, x2 = _flat_x(xstack, self.in_features)
         assert x2.shape[0] % self.K == 0
         n = x2.shape[0] // self.K
         y = torch.empty((n, self.out_features), dtype=torch.float32,
                         device=x2.device)
-        self._cat._gemv(x2, y, out_per=self.out_per, mode=mode)
+        self._cat._apply(x2, y, out_per=self.out_per, mode=mode)
         return y.reshape(n * self.K, self.out_per) if n > 1 else \
             y.reshape(self.K, self.out_per)
 

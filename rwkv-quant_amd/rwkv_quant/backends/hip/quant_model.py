@@ -20,8 +20,9 @@ Execution per layer (every numeric step is a librwkvq_hip kernel):
   LoRA down (4 branches, one launch) -> LoRA up (one launch) ->
   wkv_prep -> wkv7_scan -> wkv_tail -> o_proj GEMV (+= residual) ->
   shift_lerp(ln2, 1 lerp) -> key GEMV (relu^2) -> value GEMV (+= residual)
-Prefill (B*T >= GEMM_MIN_BATCH_NB) runs the projections as fp16 GEMMs on
-device-dequantized weights and the LoRA products as fp16 GEMMs.
+Prefill (B*T >= GEMM_MIN_BATCH_NB) runs the projections on the MFMA GEMM
+kernel (dequantization fused into the operand load, epilogue fused, the
+r/k/v triple in one launch) and the LoRA products as fp16 GEMMs.
 
 Runtime switches (module attributes, as the reference's FUSE flags):
   FUSE        fuse r/k/v into one GEMV launch at decode
@@ -272,15 +273,14 @@ class QuantBlock:
 
 
 def _apply(lin, x2, y, mode, n=None, x_ld=0):
-    """y <- epi(x2 @ W^T): GEMV kernel for small N, GEMM for prefill."""
+    """y <- epi(x2 @ W^T): GEMV kernel for small N, MFMA GEMM for prefill
+    (both with the epilogue fused)."""
+    if not isinstance(lin, DenseLinear):
+        return lin.apply_into(x2, y, mode=mode, n=n, x_ld=x_ld)
     N = n if n is not None else x2.shape[0]
-    if N < GEMM_MIN_BATCH_NB and not isinstance(lin, DenseLinear):
-        lin.gemv_into(x2, y, mode=mode, n=n, x_ld=x_ld)
-        return y
     if x_ld:
         x2 = torch.as_strided(x2, (N, lin.in_features), (x_ld, 1))
-    out = lin(x2.contiguous()) if not isinstance(lin, DenseLinear) \
-        else lin(x2)
+    out = lin(x2)
     if mode == _lib.EPI_STORE:
         y.copy_(out)
     elif mode == _lib.EPI_ADD:
@@ -369,20 +369,18 @@ class QuantRWKV7:
                       _lib.ptr(blk.ln1_b), _lib.ptr(tshift),
                       _lib.ptr(tm.coef), 6, _lib.ptr(wk.xs),
                       _lib.ptr(tshift_out), B, T, C, st)
-            if FUSE and tm.rkv_fused is not None and N < GEMM_MIN_BATCH_NB:
-                tm.rkv_fused.gemv_into(wk.xs, wk.rkv, N, 6 * C)
+            if FUSE and tm.rkv_fused is not None and (
+                    N < GEMM_MIN_BATCH_NB
+                    or tm.rkv_fused._cat.gemm_ok(tm.rkv_fused.out_per)):
+                tm.rkv_fused.apply_into(wk.xs, wk.rkv, N, 6 * C)
             else:
                 xs_flat = wk.xs.view(N, 6 * C)
                 rkv_flat = wk.rkv.view(N, 3 * C)
                 for j, lin in enumerate((tm.r_proj, tm.k_proj, tm.v_proj)):
-                    yv = rkv_flat[:, j * C:(j + 1) * C]
-                    if N < GEMM_MIN_BATCH_NB:
-                        tmp = torch.empty(N, C, device=self.device)
-                        _apply(lin, xs_flat[:, j * C:], tmp, _lib.EPI_STORE,
-                               n=N, x_ld=6 * C)
-                    else:
-                        tmp = lin(wk.xs[:, j].contiguous())
-                    yv.copy_(tmp)
+                    tmp = torch.empty(N, C, device=self.device)
+                    _apply(lin, xs_flat[:, j * C:], tmp, _lib.EPI_STORE,
+                           n=N, x_ld=6 * C)
+                    rkv_flat[:, j * C:(j + 1) * C].copy_(tmp)
             tm.run_lora(wk)
             layer0 = 1 if li == 0 else 0
             if T == 1:

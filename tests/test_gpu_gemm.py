@@ -1,0 +1,128 @@
+"""GPU parity of the MFMA prefill GEMM (dequantization fused into the
+operand load) against the CPU oracle.
+
+Bars: relmax < 1e-3 against float64 x . dequant(W)^T (BASELINE tolerance
+for GEMV/GEMM; the reference gated its prefill GEMM at 2e-3 against fp16
+operands, tests/test_gemm_prefill.py:32-49), and relmax < 2e-5 against the
+float64 product of the operands the reference's prefill feeds its fp16
+matmul (x rounded to fp16, W = the format's fp16 dequant; rtn8: the codes,
+with the fp32 row scale applied to the sum) -- so the pairing of x and W
+along k, the per-group scales and the tile bookkeeping are pinned, not just
+the overall magnitude."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import codec_ref as cr
+from rwkv_quant.backends.hip import _lib
+from rwkv_quant.backends.hip.quant_linear import (
+    GwQuantLinear, GwQuantLinearFused, QuantLinearV2, SymQuantLinear,
+    SymQuantLinearFused)
+
+from _util import act, qt_for, relmax, weights
+
+pytestmark = pytest.mark.gpu
+
+LIN = {"sb6": GwQuantLinear, "sym": SymQuantLinear, "rtn": QuantLinearV2}
+FORMATS = [("sb6", 4), ("sb6", 5), ("sb6", 6), ("sym", 6), ("sym", 8),
+           ("rtn", 8)]
+
+
+def _w(rows, cols, seed, degenerate=False, outliers=2):
+    w = weights(rows, cols, seed=seed, outlier_cols=outliers)
+    if degenerate:
+        w[3] = 0.0
+        w[5] = 1e-9
+        w[6, :256] = 0.0
+    return w
+
+
+def _gemm(lin, x, mode=_lib.EPI_STORE, y=None):
+    M = x.shape[0]
+    if y is None:
+        y = torch.empty(M, lin.out_features, device="cuda")
+    lin._run("gemm", x, y, mode=mode, n=M)
+    return y
+
+
+def _operand_ref(kind, lin, qt, x):
+    """float64 product of the fp16 operands of the reference's prefill."""
+    x16 = x.half().double().numpy()
+    if kind == "rtn":
+        q = qt.codes.double().numpy()
+        s = qt.scale.float().double().numpy().reshape(1, -1)
+        return (x16 @ q.T) * s
+    w16 = lin._dequant_w(torch.float16).cpu().double().numpy()
+    return x16 @ w16.T
+
+
+@pytest.mark.parametrize("kind,bits", FORMATS)
+@pytest.mark.parametrize("shape", [(2048, 2048), (8192, 2048), (2048, 8192),
+                                   (384, 2560)])
+@pytest.mark.parametrize("M", [128, 200, 512])
+def test_gemm_relmax(kind, bits, shape, M):
+    print(f"gemm {kind}@{bits} {shape} M={M}", flush=True)
+    w = _w(*shape, seed=shape[0] + bits, degenerate=(M == 200))
+    qt = qt_for(kind, bits, w)
+    lin = LIN[kind](qt)
+    x = act(M, shape[1], seed=M)
+    y = _gemm(lin, x.cuda()).cpu().numpy()
+    ref = cr.gemv_ref(x.numpy(), cr.dequant_qt(qt))
+    assert relmax(y, ref) < 1e-3
+    assert relmax(y, ref * 1.01) > 1e-3      # the check can fail
+    assert relmax(y, _operand_ref(kind, lin, qt, x)) < 2e-5
+
+
+@pytest.mark.parametrize("kind,bits", [("sb6", 5), ("sym", 6), ("rtn", 8)])
+@pytest.mark.parametrize("mode", [_lib.EPI_ADD, _lib.EPI_RELU2, _lib.EPI_TANH,
+                                  _lib.EPI_SIGMOID])
+def test_gemm_epilogues(kind, bits, mode):
+    lin = LIN[kind](qt_for(kind, bits, _w(1024, 2048, seed=3)))
+    x = act(160, 2048, seed=4).cuda()
+    base = _gemm(lin, x)
+    y0 = torch.randn(160, 1024, device="cuda")
+    y = _gemm(lin, x, mode=mode, y=y0.clone())
+    expect = {_lib.EPI_ADD: y0 + base, _lib.EPI_RELU2: torch.relu(base) ** 2,
+              _lib.EPI_TANH: torch.tanh(base),
+              _lib.EPI_SIGMOID: torch.sigmoid(base)}[mode]
+    assert torch.allclose(y, expect, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("kind,bits", [("sb6", 5), ("sym", 8), ("sb6", 4)])
+def test_gemm_fused_rkv_equals_separate(kind, bits):
+    """Three matrices on three input segments of a strided x (the model's
+    [T, 6, C] lerp buffer) in one launch == three launches, bit for bit."""
+    lins = [LIN[kind](qt_for(kind, bits, _w(2048, 2048, seed=s)))
+            for s in range(3)]
+    fused = (GwQuantLinearFused if kind == "sb6" else SymQuantLinearFused)(lins)
+    T = 192
+    xs = act(T * 6, 2048, seed=9).reshape(T, 6, 2048).cuda()
+    y = torch.empty(T, 3 * 2048, device="cuda")
+    fused.apply_into(xs, y, T, 6 * 2048)
+    for j, lin in enumerate(lins):
+        yj = _gemm(lin, xs[:, j].contiguous())
+        assert torch.equal(y[:, j * 2048:(j + 1) * 2048], yj)
+
+
+def test_linear_call_takes_gemm_from_128_rows():
+    """__call__ switches to the GEMM at GEMM_MIN_BATCH_NB rows; both paths
+    agree with the oracle."""
+    qt = qt_for("sym", 6, _w(2048, 2048, seed=21))
+    lin = SymQuantLinear(qt)
+    ref_w = cr.dequant_qt(qt)
+    for M in (127, 128):
+        x = act(M, 2048, seed=M)
+        y = lin(x.cuda()).cpu().numpy()
+        assert relmax(y, cr.gemv_ref(x.numpy(), ref_w)) < 1e-3
+
+
+def test_gemm_shape_errors_raise():
+    lin = GwQuantLinear(qt_for("sb6", 4, _w(192, 512, seed=1)))
+    x = torch.zeros(128, 512, device="cuda")
+    y = torch.empty(128, 192, device="cuda")
+    with pytest.raises(_lib.HipKernelError):       # 192 rows: not 128-tiled
+        lin._run("gemm", x, y, n=128)
+    with pytest.raises(_lib.HipKernelError):       # IN not a multiple of 256
+        _lib.call("rwkvq_gemm_sb6", _lib.ptr(lin.nib), None,
+                  _lib.ptr(lin.rec), 4, 128, 500, 128, _lib.ptr(x), 0,
+                  _lib.ptr(y), 128, 0, _lib.stream_handle())
