@@ -54,16 +54,88 @@ struct GemmArgs {
   float* y;              // y[t * N + n]
   long x_ld;
   int M, N, in, out_per, mode;
+  int nt, mt;            // tile counts along N and M
 };
 
 constexpr int kStepK = 128;                 // columns per K step
 constexpr int kRowH = kStepK + 8;           // LDS row stride in halves
+
+// Register pin: an empty volatile asm that "rewrites" v.  Placed after a
+// scheduling barrier, it keeps every consumer of a prefetched register (and
+// the wait for its load) behind that point.
+__device__ __forceinline__ void pin(uint32_t& v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void pin(float& v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void pin(uint4& v) { pin(v.x); pin(v.y); pin(v.z); pin(v.w); }
+__device__ __forceinline__ void pin(float4& v) { pin(v.x); pin(v.y); pin(v.z); pin(v.w); }
 
 __device__ __forceinline__ uint32_t h2_bits(h2_t v) {
   return __builtin_bit_cast(uint32_t, v);
 }
 __device__ __forceinline__ h2_t as_h2(uint32_t u) {
   return __builtin_bit_cast(h2_t, u);
+}
+
+// Raw bytes of one row's two consecutive groups (2j, 2j+1) -- one lane's
+// share of a K step -- in as few, wide loads as the layout allows: the two
+// groups share their superblock record / d, and their high-bit words and
+// block scales are adjacent.
+struct Raw2 {
+  uint4 q[4];     // nibbles: q[0], q[1]; int8 codes: q[0..1], q[2..3]
+  uint4 hb;       // high-bit words of both groups
+  uint4 rec;      // sb6 superblock record
+  uint32_t qs;    // sym: the 4 int8 block scales
+  uint32_t d;     // sym: fp16 d bits
+};
+
+__device__ __forceinline__ void pin(Raw2& r) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) pin(r.q[i]);
+  pin(r.hb); pin(r.rec); pin(r.qs); pin(r.d);
+}
+
+template <int FMT>
+__device__ __forceinline__ void load_raw2(const GemmArgs& a, int row, int ng,
+                                          int nsb, int g, Raw2& r) {
+  if (FMT == F_SYM8 || FMT == F_RTN8) {
+    const uint8_t* p = a.q + (size_t)row * a.in + g * 32;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r.q[i] = ld16(p + 16 * i);
+  } else {
+    const uint8_t* p = a.q + ((size_t)row * ng + g) * 16;
+    r.q[0] = ld16(p);
+    r.q[1] = ld16(p + 16);
+  }
+  if (FMT <= F_SB6_6)
+    r.rec = ld16(a.rec + ((size_t)row * nsb + (g >> 3)) * 16);
+  if (FMT == F_SB6_5) {
+    const uint2 v = *reinterpret_cast<const uint2*>(a.hb + (size_t)row * ng + g);
+    r.hb.x = v.x; r.hb.y = v.y;
+  }
+  if (FMT == F_SB6_6 || FMT == F_SYM6)
+    r.hb = ld16(a.hb + ((size_t)row * ng + g) * 2);
+  if (FMT == F_SYM6 || FMT == F_SYM8) {
+    r.qs = *reinterpret_cast<const uint32_t*>(a.qs + (size_t)row * (a.in >> 4) + 2 * g);
+    r.d = a.d[(size_t)row * nsb + (g >> 3)];
+  }
+}
+
+// Group gi (0, 1) of a Raw2 in the single-group form the decoder takes.
+template <int FMT>
+__device__ __forceinline__ Raw group_of(const Raw2& w, int gi) {
+  Raw r;
+  if (FMT == F_SYM8 || FMT == F_RTN8) {
+    r.a = w.q[2 * gi];
+    r.b = w.q[2 * gi + 1];
+  } else {
+    r.a = w.q[gi];
+  }
+  if (FMT <= F_SB6_6) r.b = w.rec;
+  if (FMT == F_SB6_5) r.h.x = gi ? w.hb.y : w.hb.x;
+  if (FMT == F_SB6_6 || FMT == F_SYM6)
+    r.h = gi ? make_uint2(w.hb.z, w.hb.w) : make_uint2(w.hb.x, w.hb.y);
+  r.s = gi ? (w.qs >> 16) : (w.qs & 0xFFFFu);
+  r.dd = w.d;
+  return r;
 }
 
 // fp16 weights of one (row, group) in the decoder's pair order.
@@ -92,7 +164,7 @@ __device__ __forceinline__ void dequant_group(const Raw& r, int kb,
       w[i] = h2_bits(__builtin_elementwise_fma(q, s2, m2));  // one rounding
     }
   } else if (FMT == F_SYM6 || FMT == F_SYM8) {
-    const float d = f16_bits_to_f32(r.s >> 16);
+    const float d = f16_bits_to_f32(r.dd);
     const _Float16 sa = (_Float16)((float)(int8_t)(r.s & 0xFFu) * d);
     const _Float16 sb = (_Float16)((float)(int8_t)((r.s >> 8) & 0xFFu) * d);
     const _Float16 mb = (_Float16)magic_bias<FMT>();
@@ -139,8 +211,21 @@ gemm_kernel(GemmArgs a) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 31, h = lane >> 5;
-  const int n0 = blockIdx.x * BN;
-  const int m0 = blockIdx.y * BM;
+  // Tile order: workgroup b runs on XCD b % 8 (round-robin dispatch).  The
+  // M tiles of one N tile go to the same XCD back to back, so that XCD's L2
+  // serves the W tile to all of them after one HBM read; N tiles are dealt
+  // across the XCDs.
+  int nt, mt;
+  if ((a.nt & 7) == 0) {
+    const int slot = blockIdx.x >> 3;
+    mt = slot % a.mt;
+    nt = (slot / a.mt) * 8 + (blockIdx.x & 7);
+  } else {
+    mt = blockIdx.x % a.mt;
+    nt = blockIdx.x / a.mt;
+  }
+  const int n0 = nt * BN;
+  const int m0 = mt * BM;
   const int seg = n0 / a.out_per;
   const int ng = a.in >> 5, nsb = a.in >> 8;
   const int nsteps = a.in / kStepK;
@@ -171,18 +256,16 @@ gemm_kernel(GemmArgs a) {
     }
   };
 
-  // ---- weights: WN rows x 2 groups per lane per step
+  // ---- weights: WN rows x 2 groups per lane per step, in registers
   int rows[WN];
 #pragma unroll
   for (int ni = 0; ni < WN; ++ni)
     rows[ni] = n0 + wave * 32 * WN + ni * 32 + r;
-  Raw cur[WN][2], nxt[WN][2];
-  auto load_w = [&](int c, Raw (&dst)[WN][2]) {
+  Raw2 cur[WN], nxt[WN];
+  auto load_w = [&](int c, Raw2 (&dst)[WN]) {
 #pragma unroll
     for (int ni = 0; ni < WN; ++ni)
-#pragma unroll
-      for (int gi = 0; gi < 2; ++gi)
-        load_raw<FMT>(a, rows[ni], ng, nsb, c * 4 + 2 * h + gi, dst[ni][gi]);
+      load_raw2<FMT>(a, rows[ni], ng, nsb, c * 4 + 2 * h, dst[ni]);
   };
 
   f32x16_t acc[WM][WN];
@@ -202,13 +285,17 @@ gemm_kernel(GemmArgs a) {
     const int cn = min(c + 1, nsteps - 1);     // clamped: loads stay in W / x
     load_w(cn, nxt);
     load_x(cn);
+    // keep the loads of step c + 1 ahead of this step's MFMAs: left to
+    // itself the scheduler sinks them next to their use
+    __builtin_amdgcn_sched_barrier(0);
     const _Float16* xs = sx[c & 1];
 #pragma unroll
     for (int gi = 0; gi < 2; ++gi) {
       uint32_t w[WN][16];
       const int kb = (c * 4 + 2 * h + gi) & 7;   // group within superblock
 #pragma unroll
-      for (int ni = 0; ni < WN; ++ni) dequant_group<FMT>(cur[ni][gi], kb, w[ni]);
+      for (int ni = 0; ni < WN; ++ni)
+        dequant_group<FMT>(group_of<FMT>(cur[ni], gi), kb, w[ni]);
 #pragma unroll
       for (int ss = 0; ss < 4; ++ss) {
         half8_t bx[WM];
@@ -228,12 +315,16 @@ gemm_kernel(GemmArgs a) {
         }
       }
     }
+    // the prefetched registers are consumed only from here on
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int p = 0; p < XI; ++p) { pin(xa[p]); pin(xbv[p]); }
+#pragma unroll
+    for (int ni = 0; ni < WN; ++ni) pin(nxt[ni]);
     store_x((c + 1) & 1);
     __syncthreads();
 #pragma unroll
-    for (int ni = 0; ni < WN; ++ni)
-#pragma unroll
-      for (int gi = 0; gi < 2; ++gi) cur[ni][gi] = nxt[ni][gi];
+    for (int ni = 0; ni < WN; ++ni) cur[ni] = nxt[ni];
   }
 
   // ---- epilogue: lane holds tokens m0 + 32 mi + r, rows 4 at a time
@@ -283,8 +374,11 @@ gemm_kernel(GemmArgs a) {
 
 template <int FMT, int WN, int WM>
 int launch_tile(const GemmArgs& a, hipStream_t s) {
-  dim3 grid(a.N / (128 * WN), (a.M + 32 * WM - 1) / (32 * WM));
-  hipLaunchKernelGGL((gemm_kernel<FMT, WN, WM>), grid, dim3(256), 0, s, a);
+  GemmArgs b = a;
+  b.nt = a.N / (128 * WN);
+  b.mt = (a.M + 32 * WM - 1) / (32 * WM);
+  hipLaunchKernelGGL((gemm_kernel<FMT, WN, WM>), dim3(b.nt * b.mt),
+                     dim3(256), 0, s, b);
   return hipGetLastError() == hipSuccess ? RWKVQ_OK : RWKVQ_ERR_LAUNCH;
 }
 

@@ -190,7 +190,7 @@ gemv_kernel(GemvArgs a) {
         for (int n = 0; n < NN; ++n)
           acc[n][j] = active ? s * (dA[n] + dB[n]) + m * xsf[n] : 0.f;
       } else if (FMT == F_SYM6 || FMT == F_SYM8) {
-        float d = f16_bits_to_f32(cur[j].s >> 16);
+        float d = f16_bits_to_f32(cur[j].dd);
         float sA = f16_round((float)(int8_t)(cur[j].s & 0xFFu) * d);
         float sB = f16_round((float)(int8_t)((cur[j].s >> 8) & 0xFFu) * d);
 #pragma unroll

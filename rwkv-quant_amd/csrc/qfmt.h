@@ -38,7 +38,10 @@ struct Raw {
   uint4 a;        // nibbles, or codes 0..15 (int8 formats)
   uint4 b;        // sb6 superblock record, or codes 16..31 (int8 formats)
   uint2 h;        // high-bit words
-  uint32_t s;     // sym: qs pair (low 16 bits) | d (high 16 bits)
+  uint32_t s;     // sym: qs pair (two int8 block scales, low 16 bits)
+  uint32_t dd;    // sym: fp16 d bits
+  // loaded values are kept as loaded (no arithmetic at load time), so a
+  // consumer's wait is for its own loads, not for the whole batch
 };
 
 template <int FMT, class Args>
@@ -58,10 +61,9 @@ __device__ __forceinline__ void load_raw(const Args& a, int row, int ng,
   if (FMT == F_SB6_6 || FMT == F_SYM6)
     r.h = *reinterpret_cast<const uint2*>(a.hb + (size_t)row * ng * 2 + g * 2);
   if (FMT == F_SYM6 || FMT == F_SYM8) {
-    uint32_t q2 = *reinterpret_cast<const uint16_t*>(
+    r.s = *reinterpret_cast<const uint16_t*>(
         a.qs + (size_t)row * (a.in >> 4) + 2 * g);
-    uint32_t dd = a.d[(size_t)row * nsb + (g >> 3)];
-    r.s = q2 | (dd << 16);
+    r.dd = a.d[(size_t)row * nsb + (g >> 3)];
   }
 }
 
