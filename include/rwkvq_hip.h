@@ -227,6 +227,25 @@ int rwkvq_wkv7_decode(const float* rkv, const float* yw, const float* ya,
                       const float* state_in, float* state_out, float* out,
                       int B, int H, int head_size, void* stream);
 
+/* Decode core with the LoRA up products folded in: as rwkvq_wkv7_decode,
+ * with the branch outputs computed per head from the down outputs
+ * h[k] [B, rank[k]] (after their nonlinearity) and the up matrices
+ * Bup[k] fp16 [D, rank[k]], k = 0..3 for w, a, v, g (v unused in layer 0,
+ * may be null there).  h is rounded to fp16 pairs, products fp32.
+ * rank[k] % 8 == 0, rank[k] <= 512.
+ * Replaces: the decode path of _forward_stateful_fused from the LoRA down
+ * outputs to the o_proj input, including QuantTMix._lora's up products
+ * (reference: quant_model.py:462-526, 693-720). */
+int rwkvq_wkv7_decode_lora(const float* rkv, const float* const* h,
+                           const void* const* Bup, const int* rank,
+                           const float* w0, const float* a0, const float* v0,
+                           const float* k_k, const float* k_a,
+                           const float* r_k, const float* ln_w,
+                           const float* ln_b, float* v_first, int layer0,
+                           const float* state_in, float* state_out,
+                           float* out, int B, int H, int head_size,
+                           void* stream);
+
 /* Grouped dense-fp16 GEMV of up to 4 low-rank branches in one launch:
  * y_j[n, r] = epi_j( sum_c x_j[n * x_ld_j + c] * W_j[r, c] ), n < N <= 8.
  * in_j % 16 == 0 and in_j <= 512, or in_j in {2048, 2560}.
@@ -236,6 +255,7 @@ int rwkvq_lora_gemv(int n_jobs, const void* const* W, const float* const* x,
                     const int* x_ld, float* const* y, const int* y_ld,
                     const int* rows, const int* in, const int* epi, int N,
                     void* stream);
+
 
 /* ------------------------------------------------------------- probes
  * HBM read ceiling: stream `bytes` (multiple of 16) with 16-byte loads

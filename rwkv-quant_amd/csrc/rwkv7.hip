@@ -335,6 +335,17 @@ wkv_tail_k(const float* __restrict__ y, const float* __restrict__ rkv,
 // gate tail in one launch.  256 threads: thread (row i = tid / 4, part
 // p = tid % 4) owns S[i][16 p .. 16 p + 16); wave 0 handles the per-channel
 // work of the head's 64 channels.
+// LoRA up products folded into the decode core: branch k (w, a, v, g) of
+// token b is B_k [D, r_k] (fp16) times the down-projection output
+// h_k[b, :r_k] (after its nonlinearity), for the head's 64 channels.
+struct LoraUp {
+  const float* h[4];
+  const uint16_t* B[4];
+  int r[4];
+};
+constexpr int kMaxCat = 1024;   // sum of the four ranks
+
+template <bool LORA>
 __global__ void __launch_bounds__(256)
 wkv_decode_k(const float* __restrict__ rkv, const float* __restrict__ yw,
              const float* __restrict__ ya, const float* __restrict__ yv,
@@ -344,7 +355,7 @@ wkv_decode_k(const float* __restrict__ rkv, const float* __restrict__ yw,
              const float* __restrict__ r_k, const float* __restrict__ lnw,
              const float* __restrict__ lnb, float* __restrict__ vfirst,
              int layer0, const float* state_in, float* state_out,
-             float* __restrict__ out, int H) {
+             float* __restrict__ out, int H, LoraUp lu) {
   constexpr int P = 4, C = kHead / P;
   __shared__ float4 s_w[kHead / 4], s_k[kHead / 4], s_a[kHead / 4],
       s_b[kHead / 4], s_r[kHead / 4];
@@ -362,6 +373,71 @@ wkv_decode_k(const float* __restrict__ rkv, const float* __restrict__ yw,
     float4 q = *reinterpret_cast<const float4*>(state_in + soff + c);
     S[c] = q.x; S[c + 1] = q.y; S[c + 2] = q.z; S[c + 3] = q.w;
   }
+  __shared__ float s_up[4][kHead];
+  if constexpr (LORA) {
+    // The four branches' down outputs of token bi, concatenated (w, a, v,
+    // g; an absent branch has rank 0) as fp16 pairs (the reference rounds
+    // the low-rank activations to fp16 before the up product).
+    __shared__ uint32_t s_hp[kMaxCat / 2];
+    const uint16_t* B0 = lu.B[0];
+    const uint16_t* B1 = lu.B[1];
+    const uint16_t* B2 = lu.B[2];
+    const uint16_t* B3 = lu.B[3];
+    const int r0 = lu.r[0], r1 = lu.r[1], r2 = lu.r[2], r3 = lu.r[3];
+    const int o1 = r0, o2 = o1 + r1, o3 = o2 + r2, R = o3 + r3;
+    for (int p = tid; 2 * p < R; p += 256) {
+      const int o = 2 * p;
+      const float* hk = o < o1 ? lu.h[0] : o < o2 ? lu.h[1]
+                      : o < o3 ? lu.h[2] : lu.h[3];
+      const int rk = o < o1 ? r0 : o < o2 ? r1 : o < o3 ? r2 : r3;
+      const int ok = o < o1 ? 0 : o < o2 ? o1 : o < o3 ? o2 : o3;
+      const float* src = hk + (size_t)bi * rk + (o - ok);
+      s_hp[p] = pack_h2(src[0], src[1]);
+    }
+    __syncthreads();
+    // 4 lanes per channel; lane part j takes the 8-value chunks j, j+4, ...
+    // of the concatenated rank axis, so every load of the row is issued
+    // before the first product (one memory round trip)
+    const int ch = h * kHead + (tid >> 2), j = tid & 3;
+    const int nc = R / 8;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    uint4 wv[kMaxCat / 32];
+#pragma unroll
+    for (int i = 0; i < kMaxCat / 32; ++i) {
+      const int q = j + 4 * i;
+      if (q < nc) {
+        const int o = 8 * q;
+        const uint16_t* Bk = o < o1 ? B0 : o < o2 ? B1 : o < o3 ? B2 : B3;
+        const int rk = o < o1 ? r0 : o < o2 ? r1 : o < o3 ? r2 : r3;
+        const int ok = o < o1 ? 0 : o < o2 ? o1 : o < o3 ? o2 : o3;
+        wv[i] = ld16(Bk + (size_t)ch * rk + (o - ok));
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kMaxCat / 32; ++i) {
+      const int q = j + 4 * i;
+      if (q < nc) {
+        const int o = 8 * q;
+        float d = dot2(wv[i].x, s_hp[4 * q], 0.f);
+        d = dot2(wv[i].y, s_hp[4 * q + 1], d);
+        d = dot2(wv[i].z, s_hp[4 * q + 2], d);
+        d = dot2(wv[i].w, s_hp[4 * q + 3], d);
+        if (o < o1) acc[0] += d;
+        else if (o < o2) acc[1] += d;
+        else if (o < o3) acc[2] += d;
+        else acc[3] += d;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      acc[k] += dpp_f<0xB1>(acc[k]);       // quad_perm [1,0,3,2]
+      acc[k] += dpp_f<0x4E>(acc[k]);       // quad_perm [2,3,0,1]
+    }
+    // lane part j stores branch j of its channel
+    s_up[j][tid >> 2] = j == 0 ? acc[0] : j == 1 ? acc[1]
+                      : j == 2 ? acc[2] : acc[3];
+    __syncthreads();
+  }
   float vp = 0.f, gc = 0.f, lw = 0.f, lb = 0.f;
   if (tid < kHead) {
     const int c = h * kHead + tid;
@@ -369,14 +445,18 @@ wkv_decode_k(const float* __restrict__ rkv, const float* __restrict__ yw,
     const float r = rkv[(size_t)bi * 3 * D + c];
     const float k = rkv[(size_t)bi * 3 * D + D + c];
     float v = rkv[(size_t)bi * 3 * D + 2 * D + c];
-    const float wv = __expf(-0.606531f * sigm(yw[e] + w0[c]));
-    const float av = sigm(ya[e] + a0[c]);
+    const float ywe = LORA ? s_up[0][tid] : yw[e];
+    const float yae = LORA ? s_up[1][tid] : ya[e];
+    const float wv = __expf(-0.606531f * sigm(ywe + w0[c]));
+    const float av = sigm(yae + a0[c]);
     const float kkr = k * k_k[c];
     const float kk = kkr / sqrtf(wave_sum_dpp(kkr * kkr) + 1e-12f);
     const float kp = k * (1.f + (av - 1.f) * k_a[c]);
-    gc = g[e]; lw = lnw[c]; lb = lnb[c];
+    gc = LORA ? s_up[3][tid] : g[e];
+    lw = lnw[c]; lb = lnb[c];
     const float rkc = r_k[c];
-    if (!layer0) v = v + (vfirst[e] - v) * sigm(yv[e] + v0[c]);
+    if (!layer0)
+      v = v + (vfirst[e] - v) * sigm((LORA ? s_up[2][tid] : yv[e]) + v0[c]);
     else vfirst[e] = v;
     const float dp = wave_sum_dpp(r * kp * rkc);
     reinterpret_cast<float*>(s_w)[tid] = wv;
@@ -512,10 +592,41 @@ int rwkvq_wkv7_decode(const float* rkv, const float* yw, const float* ya,
                       int B, int H, int head_size, void* stream) {
   if (B <= 0 || H <= 0 || head_size != kHead || (!layer0 && (!yv || !v0)))
     return RWKVQ_ERR_ARG;
-  hipLaunchKernelGGL(wkv_decode_k, dim3(B * H), dim3(256), 0,
+  hipLaunchKernelGGL(wkv_decode_k<false>, dim3(B * H), dim3(256), 0,
                      (hipStream_t)stream, rkv, yw, ya, yv, g, w0, a0, v0, k_k,
                      k_a, r_k, ln_w, ln_b, v_first, layer0,
-                     state_in ? state_in : state_out, state_out, out, H);
+                     state_in ? state_in : state_out, state_out, out, H,
+                     LoraUp{});
+  return ok_launch();
+}
+
+int rwkvq_wkv7_decode_lora(const float* rkv, const float* const* h,
+                           const void* const* Bup, const int* rank,
+                           const float* w0, const float* a0, const float* v0,
+                           const float* k_k, const float* k_a,
+                           const float* r_k, const float* ln_w,
+                           const float* ln_b, float* v_first, int layer0,
+                           const float* state_in, float* state_out,
+                           float* out, int B, int H, int head_size,
+                           void* stream) {
+  if (B <= 0 || H <= 0 || head_size != kHead) return RWKVQ_ERR_ARG;
+  LoraUp lu{};
+  for (int k = 0; k < 4; ++k) {
+    const bool need = k != 2 || !layer0;       // no v branch in layer 0
+    if (!need) continue;
+    if (!h[k] || !Bup[k] || rank[k] <= 0 || rank[k] % 8)
+      return RWKVQ_ERR_ARG;
+    lu.h[k] = h[k];
+    lu.B[k] = static_cast<const uint16_t*>(Bup[k]);
+    lu.r[k] = rank[k];
+  }
+  if (!layer0 && !v0) return RWKVQ_ERR_ARG;
+  if (lu.r[0] + lu.r[1] + lu.r[2] + lu.r[3] > kMaxCat) return RWKVQ_ERR_SIZE;
+  hipLaunchKernelGGL(wkv_decode_k<true>, dim3(B * H), dim3(256), 0,
+                     (hipStream_t)stream, rkv, nullptr, nullptr, nullptr,
+                     nullptr, w0, a0, v0, k_k, k_a, r_k, ln_w, ln_b, v_first,
+                     layer0, state_in ? state_in : state_out, state_out, out,
+                     H, lu);
   return ok_launch();
 }
 

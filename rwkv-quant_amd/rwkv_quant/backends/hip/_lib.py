@@ -48,6 +48,8 @@ SIGNATURES = {
                         _I, _I, _I, _P],
     "rwkvq_wkv_tail": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P],
     "rwkvq_lora_gemv": [_I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P],
+    "rwkvq_wkv7_decode_lora": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                               _P, _P, _I, _P, _P, _P, _I, _I, _I, _P],
     "rwkvq_wkv7_decode": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                           _P, _P, _I, _P, _P, _P, _I, _I, _I, _P],
 }

@@ -20,12 +20,16 @@ Execution per layer (every numeric step is a librwkvq_hip kernel):
   LoRA down (4 branches, one launch) -> LoRA up (one launch) ->
   wkv_prep -> wkv7_scan -> wkv_tail -> o_proj GEMV (+= residual) ->
   shift_lerp(ln2, 1 lerp) -> key GEMV (relu^2) -> value GEMV (+= residual)
+Decode (T = 1) runs LoRA up + prep + one recurrence step + tail as one
+launch per (sequence, head).
 Prefill (B*T >= GEMM_MIN_BATCH_NB) runs the projections on the MFMA GEMM
 kernel (dequantization fused into the operand load, epilogue fused, the
 r/k/v triple in one launch) and the LoRA products as fp16 GEMMs.
 
 Runtime switches (module attributes, as the reference's FUSE flags):
   FUSE        fuse r/k/v into one GEMV launch at decode
+  FUSE_DECODE decode (T = 1): the LoRA up products folded into the WKV
+              step (one launch fewer per layer)
   USE_GRAPH   replay decode steps from a captured HIP graph
 """
 import ctypes
@@ -38,6 +42,7 @@ from .quant_linear import (GEMM_MIN_BATCH_NB, DenseLinear, GwQuantLinear,
                            SymQuantLinearFused, make_linear)
 
 FUSE = True
+FUSE_DECODE = True
 USE_GRAPH = True
 LORA_KERNEL_MAX_N = 8          # rows handled by the grouped LoRA kernel
 
@@ -207,6 +212,12 @@ class QuantTMix:
                 all(lins[0].can_fuse_with(l) for l in lins):
             self.rkv_fused = SymQuantLinearFused(lins)
 
+        # decode fusion (LoRA up into the WKV step) needs ranks the fused
+        # WKV kernel tiles
+        self.decode_fusable = (
+            all(A.shape[0] % 8 == 0 for A, _ in self.lora.values())
+            and sum(A.shape[0] for A, _ in self.lora.values()) <= 1024)
+
     # order of the lerp slots in work.xs
     SLOT = {"r": 0, "k": 1, "v": 2, "w": 3, "a": 4, "g": 5}
     EPI_DOWN = {"w": _lib.EPI_TANH, "a": _lib.EPI_STORE, "v": _lib.EPI_STORE,
@@ -236,6 +247,35 @@ class QuantTMix:
             elif b == "g":
                 h = torch.sigmoid(h)
             wk.yl[b].copy_(torch.matmul(h.half(), Bm.t()).float())
+
+    def run_lora_down(self, wk):
+        """The down products only (decode with the up products folded into
+        the WKV step): one launch, results (after tanh / sigmoid) in
+        wk.h[b]."""
+        N, C = wk.N, self.C
+        br = list(self.lora)
+        xs_flat = wk.xs.view(N, 6 * C)
+        self._grouped([self.lora[b][0] for b in br],
+                      [xs_flat[:, self.SLOT[b] * C:] for b in br],
+                      [6 * C] * len(br), [wk.h[b] for b in br],
+                      [self.EPI_DOWN[b] for b in br], N)
+
+    def wkv_decode_lora(self, wk, wkv_in, wkv_out, layer0, B, H, S):
+        """Decode WKV step with the LoRA up products folded in."""
+        order = ("w", "a", "v", "g")
+        have = [b in self.lora for b in order]
+        hp = (ctypes.c_void_p * 4)(*[wk.h[b].data_ptr() if h else None
+                                     for b, h in zip(order, have)])
+        bp = (ctypes.c_void_p * 4)(*[self.lora[b][1].data_ptr() if h
+                                     else None for b, h in zip(order, have)])
+        rk = (ctypes.c_int * 4)(*[self.lora[b][0].shape[0] if h else 0
+                                  for b, h in zip(order, have)])
+        _lib.call("rwkvq_wkv7_decode_lora", _lib.ptr(wk.rkv), hp, bp, rk,
+                  _lib.ptr(self.w0), _lib.ptr(self.a0), _lib.ptr(self.v0),
+                  _lib.ptr(self.k_k), _lib.ptr(self.k_a), _lib.ptr(self.r_k),
+                  _lib.ptr(self.ln_x_w), _lib.ptr(self.ln_x_b),
+                  _lib.ptr(wk.v_first), layer0, _lib.ptr(wkv_in),
+                  _lib.ptr(wkv_out), _lib.ptr(wk.o), B, H, S, _stream())
 
     @staticmethod
     def _grouped(W, X, x_ld, Y, epi, N):
@@ -365,6 +405,7 @@ class QuantRWKV7:
             tm, cm = blk.tmix, blk.cmix
             wkv_in, tshift, cshift = state
             wkv_out, tshift_out, cshift_out = out_states[li]
+            layer0 = 1 if li == 0 else 0
             _lib.call("rwkvq_shift_lerp", _lib.ptr(x), _lib.ptr(blk.ln1_w),
                       _lib.ptr(blk.ln1_b), _lib.ptr(tshift),
                       _lib.ptr(tm.coef), 6, _lib.ptr(wk.xs),
@@ -381,9 +422,15 @@ class QuantRWKV7:
                     _apply(lin, xs_flat[:, j * C:], tmp, _lib.EPI_STORE,
                            n=N, x_ld=6 * C)
                     rkv_flat[:, j * C:(j + 1) * C].copy_(tmp)
-            tm.run_lora(wk)
-            layer0 = 1 if li == 0 else 0
-            if T == 1:
+            fused = (T == 1 and FUSE_DECODE and tm.decode_fusable
+                     and N <= LORA_KERNEL_MAX_N)
+            if fused:
+                # LoRA up folded into the WKV step: 2 launches for LoRA + WKV
+                tm.run_lora_down(wk)
+                tm.wkv_decode_lora(wk, wkv_in, wkv_out, layer0, B, H,
+                                   self.head_size)
+            elif T == 1:
+                tm.run_lora(wk)
                 _lib.call("rwkvq_wkv7_decode", _lib.ptr(wk.rkv),
                           _lib.ptr(wk.yl["w"]), _lib.ptr(wk.yl["a"]),
                           None if layer0 else _lib.ptr(wk.yl["v"]),
@@ -395,6 +442,7 @@ class QuantRWKV7:
                           _lib.ptr(wkv_out), _lib.ptr(wk.o), B, H,
                           self.head_size, st)
             else:
+                tm.run_lora(wk)
                 self._wkv_seq(tm, wk, wkv_in, wkv_out, layer0, B, T, st)
             _apply(tm.o_proj, wk.o, x, _lib.EPI_ADD)
             _lib.call("rwkvq_shift_lerp", _lib.ptr(x), _lib.ptr(blk.ln2_w),

@@ -83,10 +83,12 @@ def world_state_dict(n_layer, n_embd, head_size=64, vocab=65536, ffn=None,
 
 
 def quantized_model(preset, n_layer, n_embd, head_size=64, vocab=65536,
-                    ffn=None, seed=0, config=None, device="cpu"):
+                    ffn=None, seed=0, config=None, device="cpu",
+                    to_cpu=False):
     """Random-init model quantized with a preset -> QuantizedCheckpoint.
     With a GPU `device` the weights are drawn and quantized there (the
-    quantizer is plain torch) and only the packed fields come back."""
+    quantizer is plain torch); the packed fields stay on that device unless
+    `to_cpu` (the CPU oracle needs them on the host)."""
     from ..formats import writer
     from ..presets import PRESETS
     cfg = config if config is not None else PRESETS[preset]
@@ -95,4 +97,15 @@ def quantized_model(preset, n_layer, n_embd, head_size=64, vocab=65536,
     ck = writer.quantize_state_dict(sd, cfg, naming="world", n_layer=n_layer,
                                     n_embd=n_embd, head_size=head_size,
                                     vocab_size=vocab)
+    return checkpoint_to(ck, "cpu") if to_cpu else ck
+
+
+def checkpoint_to(ck, device):
+    """Move every tensor field of a QuantizedCheckpoint to `device`."""
+    import dataclasses
+    for qt in ck.tensors.values():
+        for f in dataclasses.fields(qt):
+            v = getattr(qt, f.name)
+            if torch.is_tensor(v):
+                setattr(qt, f.name, v.to(device))
     return ck
