@@ -48,6 +48,8 @@ extern "C" {
 #define RWKVQ_EPI_RELU2 2    /* y = relu(acc)^2 (channel-mix key) */
 #define RWKVQ_EPI_TANH 3     /* y = tanh(acc) */
 #define RWKVQ_EPI_SIGMOID 4  /* y = sigmoid(acc) */
+#define RWKVQ_EPI_PER_SEG 5  /* rwkvq_gemm_f16: mode of segment j in bits
+                                4j..4j+3 of seg_modes */
 
 /* ---------------------------------------------------------------- GEMV
  * y[n, r] = epi( sum_c x[n, r / out_per, c] * W[r, c] ),  n < n_cols.
@@ -109,6 +111,17 @@ int rwkvq_gemm_sym(const uint8_t* codes, const uint32_t* hb, const int8_t* qs,
 int rwkvq_gemm_rtn8(const int8_t* codes, const uint16_t* scale, int rows,
                     int in, int out_per, const float* x, long x_ld, float* y,
                     int M, int epilogue, void* stream);
+
+/* The same GEMM over dense fp16 rows W [rows, in] (in % 128 == 0): the
+ * prefill LoRA products.  With epilogue RWKVQ_EPI_PER_SEG each input
+ * segment j (rows j*out_per ..) applies the mode in bits 4j..4j+3 of
+ * seg_modes (up to 8 segments), so the down products of the branches
+ * (tanh / none / sigmoid) run as one launch.
+ * Replaces: QuantTMix._lora at B*T > 1, fp16 matmuls of the dense LoRA
+ * factors (reference: quant_model.py:462-526). */
+int rwkvq_gemm_f16(const uint16_t* w, int rows, int in, int out_per,
+                   const float* x, long x_ld, float* y, int M, int epilogue,
+                   int seg_modes, void* stream);
 
 /* ------------------------------------------------------ dequant to fp32
  * Bit-exact with the format's dequant formula: w = q * s + m with

@@ -54,6 +54,7 @@ struct GemmArgs {
   float* y;              // y[t * N + n]
   long x_ld;
   int M, N, in, out_per, mode;
+  int seg_modes;         // mode RWKVQ_EPI_PER_SEG: 4 bits per segment
   int nt, mt;            // tile counts along N and M
 };
 
@@ -80,22 +81,37 @@ __device__ __forceinline__ h2_t as_h2(uint32_t u) {
 // groups share their superblock record / d, and their high-bit words and
 // block scales are adjacent.
 struct Raw2 {
-  uint4 q[4];     // nibbles: q[0], q[1]; int8 codes: q[0..1], q[2..3]
+  uint4 q[8];     // nibbles: q[0], q[1]; int8 codes: q[0..1], q[2..3];
+                  // fp16: q[0..3], q[4..7]
   uint4 hb;       // high-bit words of both groups
   uint4 rec;      // sb6 superblock record
   uint32_t qs;    // sym: the 4 int8 block scales
   uint32_t d;     // sym: fp16 d bits
 };
 
-__device__ __forceinline__ void pin(Raw2& r) {
+// only the fields the format loads (pinning an unused one would keep its
+// registers alive)
+template <int FMT>
+__device__ __forceinline__ void pin_raw2(Raw2& r) {
+  constexpr int NQ = FMT == F_F16 ? 8
+                   : (FMT == F_SYM8 || FMT == F_RTN8) ? 4 : 2;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) pin(r.q[i]);
-  pin(r.hb); pin(r.rec); pin(r.qs); pin(r.d);
+  for (int i = 0; i < NQ; ++i) pin(r.q[i]);
+  if (FMT == F_SB6_5) { pin(r.hb.x); pin(r.hb.y); }
+  if (FMT == F_SB6_6 || FMT == F_SYM6) pin(r.hb);
+  if (FMT <= F_SB6_6) pin(r.rec);
+  if (FMT == F_SYM6 || FMT == F_SYM8) { pin(r.qs); pin(r.d); }
 }
 
 template <int FMT>
 __device__ __forceinline__ void load_raw2(const GemmArgs& a, int row, int ng,
                                           int nsb, int g, Raw2& r) {
+  if (FMT == F_F16) {
+    const uint8_t* p = a.q + ((size_t)row * a.in + g * 32) * 2;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r.q[i] = ld16(p + 16 * i);
+    return;
+  }
   if (FMT == F_SYM8 || FMT == F_RTN8) {
     const uint8_t* p = a.q + (size_t)row * a.in + g * 32;
 #pragma unroll
@@ -181,6 +197,22 @@ __device__ __forceinline__ void dequant_group(const Raw& r, int kb,
   }
 }
 
+// fp16 weights of group gi of a Raw2 in the decoder's pair order (dense
+// fp16 rows: the stored values, natural order).
+template <int FMT>
+__device__ __forceinline__ void weights_of(const Raw2& r2, int gi, int kb,
+                                           uint32_t w[16]) {
+  if constexpr (FMT == F_F16) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint4 v = r2.q[4 * gi + q];
+      w[4 * q] = v.x; w[4 * q + 1] = v.y; w[4 * q + 2] = v.z; w[4 * q + 3] = v.w;
+    }
+  } else {
+    dequant_group<FMT>(group_of<FMT>(r2, gi), kb, w);
+  }
+}
+
 // Columns (within a group) of the two float4s that sub-step s of the pair
 // order reads: pairs 4s..4s+3.
 template <int FMT>
@@ -193,7 +225,7 @@ __device__ __forceinline__ void step_cols(int s, int& ca, int& cb) {
 // 8 x values of one (token, group, sub-step) -> 4 fp16 pairs in pair order.
 template <int FMT>
 __device__ __forceinline__ uint4 x_pairs(float4 A, float4 B) {
-  if (FMT == F_SYM8 || FMT == F_RTN8)      // pairs (2i, 2i+1)
+  if (FMT == F_SYM8 || FMT == F_RTN8 || FMT == F_F16)   // pairs (2i, 2i+1)
     return make_uint4(pack_h2(A.x, A.y), pack_h2(A.z, A.w),
                       pack_h2(B.x, B.y), pack_h2(B.z, B.w));
   return make_uint4(pack_h2(A.x, B.x), pack_h2(A.y, B.y),   // (c0, c1)
@@ -294,8 +326,7 @@ gemm_kernel(GemmArgs a) {
       uint32_t w[WN][16];
       const int kb = (c * 4 + 2 * h + gi) & 7;   // group within superblock
 #pragma unroll
-      for (int ni = 0; ni < WN; ++ni)
-        dequant_group<FMT>(group_of<FMT>(cur[ni], gi), kb, w[ni]);
+      for (int ni = 0; ni < WN; ++ni) weights_of<FMT>(cur[ni], gi, kb, w[ni]);
 #pragma unroll
       for (int ss = 0; ss < 4; ++ss) {
         half8_t bx[WM];
@@ -320,7 +351,7 @@ gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int p = 0; p < XI; ++p) { pin(xa[p]); pin(xbv[p]); }
 #pragma unroll
-    for (int ni = 0; ni < WN; ++ni) pin(nxt[ni]);
+    for (int ni = 0; ni < WN; ++ni) pin_raw2<FMT>(nxt[ni]);
     store_x((c + 1) & 1);
     __syncthreads();
 #pragma unroll
@@ -328,6 +359,8 @@ gemm_kernel(GemmArgs a) {
   }
 
   // ---- epilogue: lane holds tokens m0 + 32 mi + r, rows 4 at a time
+  const int mode = a.mode == RWKVQ_EPI_PER_SEG
+                       ? (a.seg_modes >> (4 * seg)) & 15 : a.mode;
 #pragma unroll
   for (int mi = 0; mi < WM; ++mi) {
     const int t = m0 + mi * 32 + r;
@@ -348,7 +381,7 @@ gemm_kernel(GemmArgs a) {
           v.w *= f16_bits_to_f32(sc.y >> 16);
         }
         float4* yp = reinterpret_cast<float4*>(yrow + n);
-        switch (a.mode) {
+        switch (mode) {
           case RWKVQ_EPI_ADD: {
             const float4 o = *yp;
             v.x += o.x; v.y += o.y; v.z += o.z; v.w += o.w;
@@ -396,9 +429,10 @@ int launch_gemm(const GemmArgs& a, hipStream_t s) {
   return launch_tile<FMT, 1, 1>(a, s);
 }
 
-int check_gemm(int rows, int in, int out_per, int M, long x_ld, int mode) {
+int check_gemm(int rows, int in, int out_per, int M, long x_ld, int mode,
+               int k_mult = 256) {
   if (rows <= 0 || in <= 0 || M <= 0 || out_per <= 0) return RWKVQ_ERR_ARG;
-  if (in % 256) return RWKVQ_ERR_ARG;
+  if (in % k_mult) return RWKVQ_ERR_ARG;
   if (rows % out_per || out_per % 128) return RWKVQ_ERR_ARG;
   if (x_ld < (long)(rows / out_per) * in) return RWKVQ_ERR_ARG;
   if (mode < 0 || mode > RWKVQ_EPI_SIGMOID) return RWKVQ_ERR_ARG;
@@ -453,6 +487,25 @@ int rwkvq_gemm_rtn8(const int8_t* codes, const uint16_t* scale, int rows,
   if (st) return st;
   a.q = reinterpret_cast<const uint8_t*>(codes); a.d = scale;
   return launch_gemm<F_RTN8>(a, (hipStream_t)stream);
+}
+
+int rwkvq_gemm_f16(const uint16_t* w, int rows, int in, int out_per,
+                   const float* x, long x_ld, float* y, int M, int mode,
+                   int seg_modes, void* stream) {
+  GemmArgs a = make_args(rows, in, out_per, x, x_ld, y, M,
+                         mode == RWKVQ_EPI_PER_SEG ? 0 : mode);
+  int st = check_gemm(rows, in, out_per, M, a.x_ld, a.mode, kStepK);
+  if (st) return st;
+  if (mode == RWKVQ_EPI_PER_SEG) {
+    for (int j = 0; j < rows / out_per; ++j) {
+      const int m = (seg_modes >> (4 * j)) & 15;
+      if (m > RWKVQ_EPI_SIGMOID || j >= 8) return RWKVQ_ERR_ARG;
+    }
+    a.mode = mode;
+    a.seg_modes = seg_modes;
+  }
+  a.q = reinterpret_cast<const uint8_t*>(w);
+  return launch_gemm<F_F16>(a, (hipStream_t)stream);
 }
 
 }  // extern "C"

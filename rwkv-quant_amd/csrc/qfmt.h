@@ -16,7 +16,8 @@
 namespace rwkvq {
 
 enum Fmt { F_SB6_4 = 0, F_SB6_5 = 1, F_SB6_6 = 2, F_SYM6 = 3, F_SYM8 = 4,
-           F_RTN8 = 5 };
+           F_RTN8 = 5,
+           F_F16 = 6 };   // dense fp16 rows (GEMM only)
 
 template <int FMT>
 __device__ __forceinline__ void x_cols(int i, int& c0, int& c1) {

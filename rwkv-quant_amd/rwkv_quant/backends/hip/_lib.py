@@ -16,6 +16,7 @@ ERRORS = {1001: "invalid argument or shape", 1002: "kernel launch failed",
           1003: "size beyond a supported limit"}
 
 EPI_STORE, EPI_ADD, EPI_RELU2, EPI_TANH, EPI_SIGMOID = 0, 1, 2, 3, 4
+EPI_PER_SEG = 5                # rwkvq_gemm_f16: mode per input segment
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -32,6 +33,7 @@ SIGNATURES = {
     "rwkvq_gemm_sym": [_P, _P, _P, _P, _I, _I, _I, _I, _P, _L, _P, _I, _I,
                        _P],
     "rwkvq_gemm_rtn8": [_P, _P, _I, _I, _I, _P, _L, _P, _I, _I, _P],
+    "rwkvq_gemm_f16": [_P, _I, _I, _I, _P, _L, _P, _I, _I, _I, _P],
     "rwkvq_dequant_sb6_f32": [_P, _P, _P, _I, _I, _I, _P, _I, _P],
     "rwkvq_dequant_sym_f32": [_P, _P, _P, _P, _I, _I, _I, _P, _I, _P],
     "rwkvq_dequant_rtn8_f32": [_P, _P, _I, _I, _P, _I, _P],

@@ -136,6 +136,9 @@ class _Work:
         self.xs = torch.empty(N, 6, C, **f)      # r, k, v, w, a, g lerps
         self.rkv = torch.empty(N, 3, C, **f)
         self.h = {b: torch.empty(N, r, **f) for b, r in ranks.items()}
+        rp = -(-max(ranks.values()) // 128) * 128
+        # prefill LoRA: the down outputs of all branches, each padded to rp
+        self.h_cat = torch.empty(N, len(ranks) * rp, **f) if N > 8 else None
         self.yl = {b: torch.empty(N, C, **f) for b in ranks}
         self.w = torch.empty(N, C, **f)
         self.kp = torch.empty(N, C, **f)
@@ -239,14 +242,48 @@ class QuantTMix:
                           [wk.yl[b] for b in branches],
                           [_lib.EPI_STORE] * len(branches), N)
             return
-        for b in branches:
-            A, Bm = self.lora[b]
-            h = torch.matmul(wk.xs[:, self.SLOT[b]].half(), A.t()).float()
-            if b == "w":
-                h = torch.tanh(h)
-            elif b == "g":
-                h = torch.sigmoid(h)
-            wk.yl[b].copy_(torch.matmul(h.half(), Bm.t()).float())
+        # prefill: the MFMA GEMM over the dense fp16 factors; one launch for
+        # the down products of all branches (their lerp slots v, w, a, g are
+        # adjacent in wk.xs), one per up product
+        order, rp, A_cat, B_pad, modes = self._prefill_mats()
+        xs_flat = wk.xs.view(N, 6 * C)
+        s0 = self.SLOT[order[0]]
+        nseg = len(order)
+        _lib.call("rwkvq_gemm_f16", _lib.ptr(A_cat), nseg * rp, C, rp,
+                  _lib.ptr(xs_flat[:, s0 * C:]), 6 * C, _lib.ptr(wk.h_cat), N,
+                  _lib.EPI_PER_SEG, modes, _stream())
+        # the down GEMM wrote rows of nseg * rp values
+        hc = wk.h_cat.view(-1)[:N * nseg * rp].view(N, nseg * rp)
+        for j, b in enumerate(order):
+            _lib.call("rwkvq_gemm_f16", _lib.ptr(B_pad[b]), C, rp, C,
+                      _lib.ptr(hc[:, j * rp:]), nseg * rp,
+                      _lib.ptr(wk.yl[b]), N, _lib.EPI_STORE, 0, _stream())
+
+    def _prefill_mats(self):
+        """Prefill LoRA factors padded for the GEMM tiles (built on first
+        use): down factors stacked in lerp-slot order (v, w, a, g), each
+        padded with zero rows to rp (a multiple of 128); up factors padded
+        with zero columns to rp.  Padded outputs multiply zero weights."""
+        if getattr(self, "_pmats", None) is None:
+            order = [b for b in ("v", "w", "a", "g") if b in self.lora]
+            C = self.C
+            rp = -(-max(A.shape[0] for A, _ in self.lora.values()) // 128) * 128
+            A0 = self.lora[order[0]][0]
+            A_cat = torch.zeros(len(order) * rp, C, dtype=torch.float16,
+                                device=A0.device)
+            B_pad = {}
+            for j, b in enumerate(order):
+                A, Bm = self.lora[b]
+                r = A.shape[0]
+                A_cat[j * rp:j * rp + r] = A
+                Bp = torch.zeros(C, rp, dtype=torch.float16, device=A0.device)
+                Bp[:, :r] = Bm
+                B_pad[b] = Bp
+            modes = 0
+            for j, b in enumerate(order):
+                modes |= self.EPI_DOWN[b] << (4 * j)
+            self._pmats = (order, rp, A_cat, B_pad, modes)
+        return self._pmats
 
     def run_lora_down(self, wk):
         """The down products only (decode with the up products folded into

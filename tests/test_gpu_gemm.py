@@ -126,3 +126,36 @@ def test_gemm_shape_errors_raise():
         _lib.call("rwkvq_gemm_sb6", _lib.ptr(lin.nib), None,
                   _lib.ptr(lin.rec), 4, 128, 500, 128, _lib.ptr(x), 0,
                   _lib.ptr(y), 128, 0, _lib.stream_handle())
+
+
+@pytest.mark.parametrize("M", [24, 200, 512])
+def test_gemm_f16_dense(M):
+    """Dense fp16 rows (the prefill LoRA factors): against the float64
+    product of the fp16-rounded operands."""
+    g = torch.Generator().manual_seed(M)
+    W = (torch.randn(384, 2048, generator=g) * 0.02).half()
+    x = torch.randn(M, 2048, generator=g)
+    y = torch.empty(M, 384, device="cuda")
+    Wd, xd = W.cuda(), x.cuda()
+    _lib.call("rwkvq_gemm_f16", _lib.ptr(Wd), 384, 2048, 384, _lib.ptr(xd),
+              0, _lib.ptr(y), M, _lib.EPI_STORE, 0, _lib.stream_handle())
+    ref = x.half().double().numpy() @ W.double().numpy().T
+    assert relmax(y.cpu().numpy(), ref) < 2e-5
+
+
+def test_gemm_f16_per_segment_epilogue():
+    """Three segments of 128 rows on three input slices, modes tanh / store
+    / sigmoid (the LoRA down products of one layer in one launch)."""
+    g = torch.Generator().manual_seed(5)
+    M, K, R = 160, 256, 128
+    W = (torch.randn(3 * R, K, generator=g) * 0.1).half().cuda()
+    xs = torch.randn(M, 6, K, generator=g).cuda()
+    y = torch.empty(M, 3 * R, device="cuda")
+    modes = _lib.EPI_TANH | (_lib.EPI_STORE << 4) | (_lib.EPI_SIGMOID << 8)
+    _lib.call("rwkvq_gemm_f16", _lib.ptr(W), 3 * R, K, R,
+              _lib.ptr(xs[:, 2]), 6 * K, _lib.ptr(y), M, _lib.EPI_PER_SEG,
+              modes, _lib.stream_handle())
+    for j, f in enumerate((torch.tanh, lambda v: v, torch.sigmoid)):
+        ref = f(xs[:, 2 + j].half().float() @ W[j * R:(j + 1) * R].float().t())
+        assert torch.allclose(y[:, j * R:(j + 1) * R], ref, rtol=1e-4,
+                              atol=1e-5)
