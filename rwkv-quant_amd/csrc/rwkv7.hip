@@ -254,57 +254,61 @@ wkv_scan_k(const float* __restrict__ r, long r_ld,
     }
   };
 
+  // one recurrence step from LDS slot (buf, tt); returns y = S_t r_t of the
+  // row (all L lanes hold it after the reduction)
+  auto step = [&](int bsel, int tt) {
+    const float4 rv = sv4[bsel][tt][0][part], wv = sv4[bsel][tt][1][part],
+                 kv = sv4[bsel][tt][2][part], av = sv4[bsel][tt][3][part],
+                 bv = sv4[bsel][tt][4][part];
+    const float vi = svv[bsel][tt][il];
+    float sa = (S[0] * av.x + S[1] * av.y) + (S[2] * av.z + S[3] * av.w);
+    sa += dpp_f<0xB1>(sa);      // quad_perm [1,0,3,2]
+    sa += dpp_f<0x4E>(sa);      // quad_perm [2,3,0,1]
+    sa += dpp_f<0x141>(sa);     // row_half_mirror
+    sa += dpp_f<0x140>(sa);     // row_mirror
+    S[0] = S[0] * wv.x + sa * bv.x + vi * kv.x;
+    S[1] = S[1] * wv.y + sa * bv.y + vi * kv.y;
+    S[2] = S[2] * wv.z + sa * bv.z + vi * kv.z;
+    S[3] = S[3] * wv.w + sa * bv.w + vi * kv.w;
+    float yp = (S[0] * rv.x + S[1] * rv.y) + (S[2] * rv.z + S[3] * rv.w);
+    yp += dpp_f<0xB1>(yp);
+    yp += dpp_f<0x4E>(yp);
+    yp += dpp_f<0x141>(yp);
+    yp += dpp_f<0x140>(yp);
+    return yp;
+  };
+
   fetch(0);
   stash(0);
   __syncthreads();
   int buf = 0;
-  float4 pr = make_float4(0.f, 0.f, 0.f, 0.f);   // r of the previous step
   for (int t0 = 0; t0 < T; t0 += TC) {
     const bool more = t0 + TC < T;
     if (more) fetch(t0 + TC);                        // in flight meanwhile
     const int n = min(TC, T - t0);
-    // LDS operands of step tt+1 are read while step tt computes.  The
-    // output of step tt-1 (S r over the state entering step tt) is reduced
-    // together with step tt's (S a): two independent DPP chains interleave
-    // instead of running back to back.
-    float4 rv = sv4[buf][0][0][part], wv = sv4[buf][0][1][part],
-           kv = sv4[buf][0][2][part], av = sv4[buf][0][3][part],
-           bv = sv4[buf][0][4][part];
-    float vi = svv[buf][0][il];
-    for (int tt = 0; tt < n; ++tt) {
-      const int tn = min(tt + 1, TC - 1);
-      const float4 rn = sv4[buf][tn][0][part], wn = sv4[buf][tn][1][part],
-                   kn = sv4[buf][tn][2][part], an = sv4[buf][tn][3][part],
-                   bn = sv4[buf][tn][4][part];
-      const float vn = svv[buf][tn][il];
-      float sa = (S[0] * av.x + S[1] * av.y) + (S[2] * av.z + S[3] * av.w);
-      float yp = (S[0] * pr.x + S[1] * pr.y) + (S[2] * pr.z + S[3] * pr.w);
-      sa += dpp_f<0xB1>(sa);      yp += dpp_f<0xB1>(yp);    // xor 1
-      sa += dpp_f<0x4E>(sa);      yp += dpp_f<0x4E>(yp);    // xor 2
-      sa += dpp_f<0x141>(sa);     yp += dpp_f<0x141>(yp);   // 8-mirror
-      sa += dpp_f<0x140>(sa);     yp += dpp_f<0x140>(yp);   // 16-mirror
-      if (part == 0 && (t0 + tt) > 0)
-        y[((size_t)bi * T + t0 + tt - 1) * y_ld + col0 + i] = yp;
-      S[0] = S[0] * wv.x + sa * bv.x + vi * kv.x;
-      S[1] = S[1] * wv.y + sa * bv.y + vi * kv.y;
-      S[2] = S[2] * wv.z + sa * bv.z + vi * kv.z;
-      S[3] = S[3] * wv.w + sa * bv.w + vi * kv.w;
-      pr = rv;
-      rv = rn; wv = wn; kv = kn; av = an; bv = bn; vi = vn;
+    if (n == TC) {
+      // full chunk, unrolled: the step's y reduction overlaps the next
+      // step's (S a) reduction, and lane p keeps the y of steps p, p + L
+      float ybuf[TC / L];
+#pragma unroll
+      for (int tt = 0; tt < TC; ++tt) {
+        const float yp = step(buf, tt);
+        ybuf[tt / L] = part == (tt % L) ? yp : ybuf[tt / L];
+      }
+#pragma unroll
+      for (int j = 0; j < TC / L; ++j)
+        y[((size_t)bi * T + t0 + j * L + part) * y_ld + col0 + i] = ybuf[j];
+    } else {
+      for (int tt = 0; tt < n; ++tt) {
+        const float yp = step(buf, tt);
+        if (part == 0) y[((size_t)bi * T + t0 + tt) * y_ld + col0 + i] = yp;
+      }
     }
     if (more) {
       stash(buf ^ 1);
       __syncthreads();
       buf ^= 1;
     }
-  }
-  {   // output of the last step
-    float yp = (S[0] * pr.x + S[1] * pr.y) + (S[2] * pr.z + S[3] * pr.w);
-    yp += dpp_f<0xB1>(yp);
-    yp += dpp_f<0x4E>(yp);
-    yp += dpp_f<0x141>(yp);
-    yp += dpp_f<0x140>(yp);
-    if (part == 0) y[((size_t)bi * T + T - 1) * y_ld + col0 + i] = yp;
   }
   *reinterpret_cast<float4*>(state + soff) = make_float4(S[0], S[1], S[2],
                                                          S[3]);
