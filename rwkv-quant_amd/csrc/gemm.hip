@@ -61,21 +61,6 @@ struct GemmArgs {
 constexpr int kStepK = 128;                 // columns per K step
 constexpr int kRowH = kStepK + 8;           // LDS row stride in halves
 
-// Register pin: an empty volatile asm that "rewrites" v.  Placed after a
-// scheduling barrier, it keeps every consumer of a prefetched register (and
-// the wait for its load) behind that point.
-__device__ __forceinline__ void pin(uint32_t& v) { asm volatile("" : "+v"(v)); }
-__device__ __forceinline__ void pin(float& v) { asm volatile("" : "+v"(v)); }
-__device__ __forceinline__ void pin(uint4& v) { pin(v.x); pin(v.y); pin(v.z); pin(v.w); }
-__device__ __forceinline__ void pin(float4& v) { pin(v.x); pin(v.y); pin(v.z); pin(v.w); }
-
-__device__ __forceinline__ uint32_t h2_bits(h2_t v) {
-  return __builtin_bit_cast(uint32_t, v);
-}
-__device__ __forceinline__ h2_t as_h2(uint32_t u) {
-  return __builtin_bit_cast(h2_t, u);
-}
-
 // Raw bytes of one row's two consecutive groups (2j, 2j+1) -- one lane's
 // share of a K step -- in as few, wide loads as the layout allows: the two
 // groups share their superblock record / d, and their high-bit words and
@@ -154,49 +139,6 @@ __device__ __forceinline__ Raw group_of(const Raw2& w, int gi) {
   return r;
 }
 
-// fp16 weights of one (row, group) in the decoder's pair order.
-template <int FMT>
-__device__ __forceinline__ void dequant_group(const Raw& r, int kb,
-                                              uint32_t w[16]) {
-  decode_raw<FMT>(r, w);
-  if (FMT <= F_SB6_6) {
-    const uint32_t rr[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
-    const int qs_word = (6 * kb) >> 5, qs_sh = (6 * kb) & 31;
-    const int qm_word = (48 + 6 * kb) >> 5, qm_sh = (48 + 6 * kb) & 31;
-    uint32_t lo = qs_word == 0 ? rr[0] : rr[1];
-    uint32_t hi = qs_word == 0 ? rr[1] : rr[2];
-    const uint32_t qsv = __builtin_amdgcn_alignbit(hi, lo, (uint32_t)qs_sh) & 63u;
-    lo = qm_word == 1 ? rr[1] : rr[2];
-    hi = qm_word == 1 ? rr[2] : rr[3];
-    const uint32_t qmv = __builtin_amdgcn_alignbit(hi, lo, (uint32_t)qm_sh) & 63u;
-    const float d = f16_bits_to_f32(rr[3] & 0xFFFFu);
-    const float dm = f16_bits_to_f32(rr[3] >> 16);
-    const _Float16 s = (_Float16)fmaxf(f16_round((float)qsv * d), 1e-8f);
-    const _Float16 m = (_Float16)((float)((int)qmv - 31) * dm);
-    const h2_t s2 = {s, s}, m2 = {m, m}, bias = {(_Float16)1024.f, (_Float16)1024.f};
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const h2_t q = as_h2(w[i]) - bias;                      // exact
-      w[i] = h2_bits(__builtin_elementwise_fma(q, s2, m2));  // one rounding
-    }
-  } else if (FMT == F_SYM6 || FMT == F_SYM8) {
-    const float d = f16_bits_to_f32(r.dd);
-    const _Float16 sa = (_Float16)((float)(int8_t)(r.s & 0xFFu) * d);
-    const _Float16 sb = (_Float16)((float)(int8_t)((r.s >> 8) & 0xFFu) * d);
-    const _Float16 mb = (_Float16)magic_bias<FMT>();
-    const h2_t bias = {mb, mb}, a2 = {sa, sa}, b2 = {sb, sb};
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const h2_t q = as_h2(w[i]) - bias;                      // exact
-      w[i] = h2_bits(q * (i < 8 ? a2 : b2));                  // one rounding
-    }
-  } else {
-    const h2_t bias = {(_Float16)1152.f, (_Float16)1152.f};
-#pragma unroll
-    for (int i = 0; i < 16; ++i) w[i] = h2_bits(as_h2(w[i]) - bias);
-  }
-}
-
 // fp16 weights of group gi of a Raw2 in the decoder's pair order (dense
 // fp16 rows: the stored values, natural order).
 template <int FMT>
@@ -211,25 +153,6 @@ __device__ __forceinline__ void weights_of(const Raw2& r2, int gi, int kb,
   } else {
     dequant_group<FMT>(group_of<FMT>(r2, gi), kb, w);
   }
-}
-
-// Columns (within a group) of the two float4s that sub-step s of the pair
-// order reads: pairs 4s..4s+3.
-template <int FMT>
-__device__ __forceinline__ void step_cols(int s, int& ca, int& cb) {
-  if (FMT <= F_SB6_6) { ca = 4 * s; cb = 4 * s + 16; }
-  else if (FMT == F_SYM6) { ca = (s < 2 ? 4 * s : 4 * s + 8); cb = ca + 8; }
-  else { ca = 8 * s; cb = 8 * s + 4; }
-}
-
-// 8 x values of one (token, group, sub-step) -> 4 fp16 pairs in pair order.
-template <int FMT>
-__device__ __forceinline__ uint4 x_pairs(float4 A, float4 B) {
-  if (FMT == F_SYM8 || FMT == F_RTN8 || FMT == F_F16)   // pairs (2i, 2i+1)
-    return make_uint4(pack_h2(A.x, A.y), pack_h2(A.z, A.w),
-                      pack_h2(B.x, B.y), pack_h2(B.z, B.w));
-  return make_uint4(pack_h2(A.x, B.x), pack_h2(A.y, B.y),   // (c0, c1)
-                    pack_h2(A.z, B.z), pack_h2(A.w, B.w));
 }
 
 template <int FMT, int WN, int WM>

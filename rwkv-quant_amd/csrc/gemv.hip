@@ -22,10 +22,17 @@
 //             rwkv_quant/backends/metal/quant_linear_gw.py:491-557,
 //             rwkv_quant/backends/metal/quant_linear_sym.py:107-247,
 //             rwkv_quant/backends/metal/quant_linear_v2.py:35-84).
+//
+// One or two input rows take this lane-dot kernel; three or more take the
+// matrix-core kernel further down (bgemv_kernel), which multiplies the
+// fp16 weights the format's dequant rounds to, like the prefill GEMM.
 #include "qfmt.h"
 #include "rwkvq_hip.h"
 
 using namespace rwkvq;
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 namespace {
 
@@ -253,6 +260,186 @@ gemv_kernel(GemvArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Small batches (2..16 input rows per launch) on the matrix cores.
+//
+// v_mfma_f32_16x16x32_f16 with A = W (16 weight rows x 32 k) and B = x^T
+// (32 k x 16 input rows): lane l = i + 16 q holds A[i][8 q + e] and
+// B[8 q + e][i] (e = 0..7) and receives D[4 q + v][i] (v = 0..3).  In a
+// 128-column step, quarter q of the wave decodes group 4 s + q of weight
+// row i into the fp16 weights the format's dequant rounds to (the values
+// the reference's batched path multiplies,
+// reference: rwkv_quant/backends/metal/quant_linear_gw.py:821-849,
+//            rwkv_quant/backends/metal/quant_linear_sym.py:433-484) and
+// loads the 32 x values of that group for input row i; both go in the
+// decoder's pair order, and MFMA j of the step takes pairs 4j..4j+3 of
+// every quarter, so the four MFMAs of a step sum the 128 columns exactly
+// once.  The k-reduction happens inside the matrix core: no lane
+// reductions, and the batch costs one B operand per step instead of one
+// dot product per input row.
+//
+// Workgroup = `ks` waves = ks slices of K over the same 16 * RT weight rows;
+// a wave runs `rpw` consecutive steps of its slice, with the weights (HBM)
+// and x (L2) of step s + 1 loaded before the MFMAs of step s.  The slices
+// meet in LDS in a fixed order (deterministic); each output element
+// depends only on its own input row, so a row's result does not depend on
+// the other rows of the batch.
+template <int FMT, int RT, int NS>
+__global__ void __launch_bounds__(512)
+bgemv_kernel(GemvArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int i = lane & 15, q = lane >> 4;
+  const int ng = a.in >> 5, nsb = a.in >> 8;
+  const int row0 = blockIdx.x * 16 * RT;
+  const int seg = row0 / a.out_per;
+  const int gw = wave * a.rpw * 4;         // first group of the wave's slice
+  const bool xon = i < a.n;
+  const float* xr = a.x + (size_t)(xon ? i : 0) * a.x_ld +
+                    (size_t)seg * a.in + q * 32;
+
+  auto load_w = [&](int g, Raw (&dst)[RT]) {
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+      load_raw<FMT>(a, row0 + 16 * rt + i, ng, nsb, g, dst[rt]);
+  };
+  // unconditional loads (lanes past the batch read input row 0 and zero
+  // their B operand later): no branches, so the compiler's load counting
+  // stays exact and a wait covers only the step it feeds
+  auto load_x = [&](int g0, float4 (&dst)[8]) {
+    const float4* p = reinterpret_cast<const float4*>(xr + (size_t)g0 * 32);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) dst[t] = p[t];
+  };
+
+  f32x4_t acc[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) acc[rt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  auto mma_step = [&](int st, Raw (&w_raw)[RT], float4 (&xv)[8]) {
+    half8_t bx[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      int ca, cb;
+      step_cols<FMT>(j, ca, cb);
+      uint4 xp = x_pairs<FMT>(xv[ca >> 2], xv[cb >> 2]);
+      if (!xon) xp = make_uint4(0u, 0u, 0u, 0u);
+      bx[j] = __builtin_bit_cast(half8_t, xp);
+    }
+    const int kb = (gw + 4 * st + q) & 7;   // group within its superblock
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      uint32_t w[16];
+      dequant_group<FMT>(w_raw[rt], kb, w);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+            __builtin_bit_cast(half8_t, make_uint4(w[4 * j], w[4 * j + 1],
+                                                   w[4 * j + 2], w[4 * j + 3])),
+            bx[j], acc[rt], 0, 0, 0);
+    }
+  };
+
+  Raw wa[RT], wb[RT];
+  float4 xa[8], xb[8];
+  if (NS == 2) {
+    // the common K = 2048 slice: both steps' loads in flight at once
+    load_w(gw + q, wa);
+    load_x(gw, xa);
+    load_w(gw + 4 + q, wb);
+    load_x(gw + 4, xb);
+    // keep the second step's loads ahead of the first step's MFMAs: left
+    // to itself the scheduler sinks them next to their use
+    __builtin_amdgcn_sched_barrier(0);
+    mma_step(0, wa, xa);
+    __builtin_amdgcn_sched_barrier(0);
+    mma_step(1, wb, xb);
+  } else {
+    // two register sets in turn (no copies between them: a copy would
+    // wait for the loads it copies).  Loads past the slice's last step
+    // are clamped to it (L2 hits, never used).
+    const int last = a.rpw - 1;
+    load_w(gw + q, wa);
+    load_x(gw, xa);
+    for (int st = 0; st < a.rpw; st += 2) {
+      load_w(gw + 4 * min(st + 1, last) + q, wb);
+      load_x(gw + 4 * min(st + 1, last), xb);
+      __builtin_amdgcn_sched_barrier(0);
+      mma_step(st, wa, xa);
+      __builtin_amdgcn_sched_barrier(0);
+      if (st + 1 > last) break;
+      load_w(gw + 4 * min(st + 2, last) + q, wa);
+      load_x(gw + 4 * min(st + 2, last), xa);
+      __builtin_amdgcn_sched_barrier(0);
+      mma_step(st + 1, wb, xb);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  // ---- K slices meet in LDS: red[wave][rt][v][lane]
+  __shared__ float red[8 * RT * 256];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+      red[(wave * RT + rt) * 256 + v * 64 + lane] = acc[rt][v];
+  __syncthreads();
+  constexpr int kRows = 16 * RT;
+  for (int idx = threadIdx.x; idx < kRows * 16; idx += a.ks * 64) {
+    const int n = idx / kRows, r = idx % kRows;   // rows fastest: coalesced
+    if (n >= a.n) break;
+    const int e = (r >> 4) * 256 + (r & 3) * 64 + n + 16 * ((r & 15) >> 2);
+    float v = 0.f;
+    for (int k = 0; k < a.ks; ++k) v += red[k * RT * 256 + e];
+    const int row = row0 + r;
+    if (FMT == F_RTN8) v *= f16_bits_to_f32(a.d[row]);
+    float* yp = a.y + (size_t)n * a.rows + row;
+    switch (a.mode) {
+      case RWKVQ_EPI_ADD: v += *yp; break;
+      case RWKVQ_EPI_RELU2: v = v > 0.f ? v * v : 0.f; break;
+      case RWKVQ_EPI_TANH: v = tanhf(v); break;
+      case RWKVQ_EPI_SIGMOID: v = 1.f / (1.f + __expf(-v)); break;
+      default: break;
+    }
+    *yp = v;
+  }
+}
+
+template <int FMT, int RT>
+int launch_bg_rt(GemvArgs a, hipStream_t s) {
+  dim3 grid(a.rows / (16 * RT)), block(64 * a.ks);
+  for (int n0 = 0; n0 < a.n; n0 += 16) {
+    GemvArgs b = a;
+    b.x = a.x + (size_t)n0 * a.x_ld;
+    b.y = a.y + (size_t)n0 * a.rows;
+    b.n = a.n - n0 < 16 ? a.n - n0 : 16;
+    if (a.rpw == 2)
+      hipLaunchKernelGGL((bgemv_kernel<FMT, RT, 2>), grid, block, 0, s, b);
+    else
+      hipLaunchKernelGGL((bgemv_kernel<FMT, RT, 0>), grid, block, 0, s, b);
+  }
+  return hipGetLastError() == hipSuccess ? RWKVQ_OK : RWKVQ_ERR_LAUNCH;
+}
+
+// K slices: the largest divisor (<= 8) of the 128-column step count; row
+// tiles: the widest that keeps >= 256 workgroups and divides a segment.
+template <int FMT>
+int launch_bg(GemvArgs a, hipStream_t s) {
+  const int steps = a.in / 128;
+  int ks = 8;
+  while (steps % ks) --ks;
+  a.ks = ks;
+  a.rpw = steps / ks;
+  // 64-row tiles only pay for the int8 formats (measured: sb6 heads are
+  // faster with 32-row tiles, int8 heads with 64)
+  constexpr bool kWide = FMT == F_SYM8 || FMT == F_RTN8;
+  if (kWide && a.out_per % 64 == 0 && a.rows / 64 >= 256)
+    return launch_bg_rt<FMT, 4>(a, s);
+  if (a.out_per % 32 == 0 && a.rows / 32 >= 256)
+    return launch_bg_rt<FMT, 2>(a, s);
+  return launch_bg_rt<FMT, 1>(a, s);
+}
+
 #ifndef RWKVQ_TARGET_WAVES
 #define RWKVQ_TARGET_WAVES 4096
 #endif
@@ -304,6 +491,10 @@ int launch_rs(GemvArgs a, hipStream_t s) {
 
 template <int FMT>
 int launch_fmt(GemvArgs a, hipStream_t s) {
+  // three or more input rows: the matrix-core kernel (16-row weight
+  // tiles); at two the lane-dot kernel is as fast or faster (measured)
+  if (a.n >= 3 && a.rows % 16 == 0 && a.out_per % 16 == 0)
+    return launch_bg<FMT>(a, s);
   const int ng = a.in / 32;
   a.ks = (ng + 63) / 64;
   if (a.ks > 8) return RWKVQ_ERR_SIZE;             // IN <= 16384

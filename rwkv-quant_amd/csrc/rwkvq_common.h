@@ -96,6 +96,14 @@ __device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
          ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
 }
 
+// Register pin: an empty volatile asm that "rewrites" v.  Placed after a
+// scheduling barrier, it keeps every consumer of a prefetched register (and
+// the wait for its load) behind that point.
+__device__ __forceinline__ void pin(uint32_t& v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void pin(float& v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void pin(uint4& v) { pin(v.x); pin(v.y); pin(v.z); pin(v.w); }
+__device__ __forceinline__ void pin(float4& v) { pin(v.x); pin(v.y); pin(v.z); pin(v.w); }
+
 __device__ __forceinline__ float h2_lo(uint32_t u) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)(u & 0xFFFFu));
 }

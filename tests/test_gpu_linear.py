@@ -3,7 +3,11 @@
 Bars: device dequant == oracle dequant bit for bit (fp32 bytes);
 GEMV relmax < 1e-3 against float64 x . dequant(W)^T (BASELINE tolerance,
 tighter than the reference's 3e-3 gate, tests/test_gw_kernel.py:29);
-fused r/k/v == three separate launches bit for bit."""
+fused r/k/v == three separate launches bit for bit.  Batches of three or
+more rows run on the matrix cores with the fp16-rounded weights: there
+also relmax < 2e-5 against the float64 product of those fp16 operands
+(pins the k pairing and the per-group scales), and each row's result is
+independent of the rest of the batch, bit for bit."""
 import numpy as np
 import pytest
 import torch
@@ -76,7 +80,7 @@ def test_dequant_asym_bit_exact():
 @pytest.mark.parametrize("kind,bits", FORMATS)
 @pytest.mark.parametrize("shape", [(2048, 2048), (8192, 2048), (2048, 8192),
                                    (512, 2560), (256, 10240), (96, 6144)])
-@pytest.mark.parametrize("n", [1, 3, 8])
+@pytest.mark.parametrize("n", [1, 2, 3, 8, 20])
 def test_gemv_relmax(kind, bits, shape, n):
     print(f"gemv {kind}@{bits} {shape} n={n}", flush=True)
     w = _w(*shape, seed=shape[0] + bits, outliers=2)
@@ -88,6 +92,29 @@ def test_gemv_relmax(kind, bits, shape, n):
     assert relmax(y, ref) < 1e-3
     # degenerate-reference control: the check must be able to fail
     assert relmax(y, ref * 1.01) > 1e-3
+    if n >= 3:
+        assert relmax(y, _operand_ref(kind, lin, qt, x)) < 2e-5
+
+
+def _operand_ref(kind, lin, qt, x):
+    """float64 product of the fp16 operands of the matrix-core path."""
+    x16 = x.half().double().numpy()
+    if kind == "rtn":
+        q = qt.codes.double().numpy()
+        s = qt.scale.float().double().numpy().reshape(1, -1)
+        return (x16 @ q.T) * s
+    return x16 @ lin._dequant_w(torch.float16).cpu().double().numpy().T
+
+
+@pytest.mark.parametrize("kind,bits", [("sb6", 5), ("sym", 6), ("rtn", 8)])
+def test_batched_rows_independent_of_batch(kind, bits):
+    """A row's output is the same bits whatever else is in the batch (and
+    wherever it sits in it, across the 16-row launch chunks)."""
+    lin = LIN[kind](qt_for(kind, bits, _w(2048, 2048, seed=31)))
+    x = act(20, 2048, seed=32).cuda()
+    y20 = lin(x)
+    y5 = lin(x[[17, 3, 9, 0, 12]].contiguous())
+    assert torch.equal(y5, y20[[17, 3, 9, 0, 12]])
 
 
 @pytest.mark.parametrize("kind,bits", [("sb6", 5), ("sym", 8), ("sb6", 4)])
