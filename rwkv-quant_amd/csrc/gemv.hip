@@ -284,8 +284,8 @@ gemv_kernel(GemvArgs a) {
 // meet in LDS in a fixed order (deterministic); each output element
 // depends only on its own input row, so a row's result does not depend on
 // the other rows of the batch.
-template <int FMT, int RT, int NS>
-__global__ void __launch_bounds__(512)
+template <int FMT, int RT, int NS, int KSMAX>
+__global__ void __launch_bounds__(64 * KSMAX)
 bgemv_kernel(GemvArgs a) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -340,10 +340,10 @@ bgemv_kernel(GemvArgs a) {
     }
   };
 
-  Raw wa[RT], wb[RT];
-  float4 xa[8], xb[8];
   if (NS == 2) {
-    // the common K = 2048 slice: both steps' loads in flight at once
+    // both steps' loads in flight at once
+    Raw wa[RT], wb[RT];
+    float4 xa[8], xb[8];
     load_w(gw + q, wa);
     load_x(gw, xa);
     load_w(gw + 4 + q, wb);
@@ -354,10 +354,28 @@ bgemv_kernel(GemvArgs a) {
     mma_step(0, wa, xa);
     __builtin_amdgcn_sched_barrier(0);
     mma_step(1, wb, xb);
+  } else if (NS > 2) {
+    // straight-line: step s + 1 loads while step s multiplies, in two
+    // register sets (compile-time indices, no copies)
+    Raw w2[2][RT];
+    float4 x2[2][8];
+    load_w(gw + q, w2[0]);
+    load_x(gw, x2[0]);
+#pragma unroll
+    for (int st = 0; st < NS; ++st) {
+      if (st + 1 < NS) {
+        load_w(gw + 4 * (st + 1) + q, w2[(st + 1) & 1]);
+        load_x(gw + 4 * (st + 1), x2[(st + 1) & 1]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      mma_step(st, w2[st & 1], x2[st & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   } else {
-    // two register sets in turn (no copies between them: a copy would
-    // wait for the loads it copies).  Loads past the slice's last step
-    // are clamped to it (L2 hits, never used).
+    // any step count: the same two register sets in a loop.  Loads past
+    // the slice's last step are clamped to it (L2 hits, never used).
+    Raw wa[RT], wb[RT];
+    float4 xa[8], xb[8];
     const int last = a.rpw - 1;
     load_w(gw + q, wa);
     load_x(gw, xa);
@@ -377,7 +395,7 @@ bgemv_kernel(GemvArgs a) {
   }
 
   // ---- K slices meet in LDS: red[wave][rt][v][lane]
-  __shared__ float red[8 * RT * 256];
+  __shared__ float red[KSMAX * RT * 256];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -405,7 +423,7 @@ bgemv_kernel(GemvArgs a) {
   }
 }
 
-template <int FMT, int RT>
+template <int FMT, int RT, int KSMAX>
 int launch_bg_rt(GemvArgs a, hipStream_t s) {
   dim3 grid(a.rows / (16 * RT)), block(64 * a.ks);
   for (int n0 = 0; n0 < a.n; n0 += 16) {
@@ -414,30 +432,43 @@ int launch_bg_rt(GemvArgs a, hipStream_t s) {
     b.y = a.y + (size_t)n0 * a.rows;
     b.n = a.n - n0 < 16 ? a.n - n0 : 16;
     if (a.rpw == 2)
-      hipLaunchKernelGGL((bgemv_kernel<FMT, RT, 2>), grid, block, 0, s, b);
+      hipLaunchKernelGGL((bgemv_kernel<FMT, RT, 2, KSMAX>), grid, block, 0, s, b);
+    else if (a.rpw == 4)
+      hipLaunchKernelGGL((bgemv_kernel<FMT, RT, 4, KSMAX>), grid, block, 0, s, b);
     else
-      hipLaunchKernelGGL((bgemv_kernel<FMT, RT, 0>), grid, block, 0, s, b);
+      hipLaunchKernelGGL((bgemv_kernel<FMT, RT, 0, KSMAX>), grid, block, 0, s, b);
   }
   return hipGetLastError() == hipSuccess ? RWKVQ_OK : RWKVQ_ERR_LAUNCH;
 }
 
-// K slices: the largest divisor (<= 8) of the 128-column step count; row
-// tiles: the widest that keeps >= 256 workgroups and divides a segment.
+// K slices: two 128-column steps per wave where up to 16 waves cover K,
+// else 16 slices (K a multiple of 2048), else the largest divisor <= 8 of
+// the step count.  More than 8 slices take 1024-thread workgroups of
+// 16-row tiles (128 VGPRs a lane).  Otherwise row tiles are the widest
+// that keep >= 256 workgroups and divide a segment.
 template <int FMT>
 int launch_bg(GemvArgs a, hipStream_t s) {
   const int steps = a.in / 128;
-  int ks = 8;
-  while (steps % ks) --ks;
+  int ks;
+  if (steps % 2 == 0 && steps / 2 <= 16) {
+    ks = steps / 2;
+  } else if (steps % 16 == 0) {
+    ks = 16;
+  } else {
+    ks = 8;
+    while (steps % ks) --ks;
+  }
   a.ks = ks;
   a.rpw = steps / ks;
+  if (ks > 8) return launch_bg_rt<FMT, 1, 16>(a, s);
   // 64-row tiles only pay for the int8 formats (measured: sb6 heads are
   // faster with 32-row tiles, int8 heads with 64)
   constexpr bool kWide = FMT == F_SYM8 || FMT == F_RTN8;
   if (kWide && a.out_per % 64 == 0 && a.rows / 64 >= 256)
-    return launch_bg_rt<FMT, 4>(a, s);
+    return launch_bg_rt<FMT, kWide ? 4 : 2, 8>(a, s);
   if (a.out_per % 32 == 0 && a.rows / 32 >= 256)
-    return launch_bg_rt<FMT, 2>(a, s);
-  return launch_bg_rt<FMT, 1>(a, s);
+    return launch_bg_rt<FMT, 2, 8>(a, s);
+  return launch_bg_rt<FMT, 1, 8>(a, s);
 }
 
 #ifndef RWKVQ_TARGET_WAVES
