@@ -482,8 +482,11 @@ template <int FMT, int RS>
 int launch_rs(GemvArgs a, hipStream_t s) {
   // rows per wave: aim for RWKVQ_TARGET_WAVES waves, at least RS rows; the
   // rows of a workgroup share one x segment (out_per multiple of them)
+  // (matrices up to 16384 row-slices: aim for half that many waves --
+  // measured faster, each workgroup's x staging then serves more rows)
   long rows_waves = (long)a.rows * a.ks;
-  int rpw = (int)(rows_waves / RWKVQ_TARGET_WAVES);
+  int rpw = (int)(rows_waves / (rows_waves <= 16384 ? RWKVQ_TARGET_WAVES / 2
+                                                    : RWKVQ_TARGET_WAVES));
   rpw = rpw < RS ? RS : (rpw / RS) * RS;
   if (rpw > RWKVQ_MAX_RPW) rpw = RWKVQ_MAX_RPW;
   while (a.rg > 1 && a.out_per % (a.rg * RS)) a.rg >>= 1;

@@ -54,6 +54,40 @@ def test_wkv7_scan_matches_oracle(B, T, H):
     assert torch.equal(st_in.cpu(), s0)          # input state untouched
 
 
+@pytest.mark.parametrize("B,T,nc,prev", [(1, 1, 6, True), (8, 1, 6, True),
+                                         (3, 1, 1, False), (1, 5, 6, True),
+                                         (2, 300, 1, True)])
+def test_shift_lerp_matches_float64(B, T, nc, prev):
+    """LN (eps 1e-5, two-pass) + token shift + lerps, over the column
+    slicing of few-row launches and the one-workgroup-per-row layout of
+    long ones; float64 reference, relative 1e-5."""
+    D = 2048
+    g = torch.Generator().manual_seed(B * 7 + T)
+    x = torch.randn(B, T, D, generator=g) * 3 + 0.5
+    lw, lb = torch.rand(D, generator=g) + 0.5, torch.randn(D, generator=g)
+    pr = torch.randn(B, D, generator=g) if prev else None
+    coef = torch.rand(nc, D, generator=g)
+    out = torch.empty(B, T, nc, D, device="cuda")
+    new_prev = torch.empty(B, D, device="cuda")
+    dev = [t.cuda() if t is not None else None for t in (x, lw, lb, pr, coef)]
+    _lib.call("rwkvq_shift_lerp", _lib.ptr(dev[0]), _lib.ptr(dev[1]),
+              _lib.ptr(dev[2]), _lib.ptr(dev[3]), _lib.ptr(dev[4]), nc,
+              _lib.ptr(out), _lib.ptr(new_prev), B, T, D,
+              _lib.stream_handle())
+    xd = x.double()
+    mu = xd.mean(-1, keepdim=True)
+    var = ((xd - mu) ** 2).mean(-1, keepdim=True)
+    xn = (xd - mu) / torch.sqrt(var + 1e-5) * lw.double() + lb.double()
+    first = pr.double()[:, None] if prev else torch.zeros(B, 1, D,
+                                                          dtype=torch.float64)
+    shift = torch.cat([first, xn[:, :-1]], 1)
+    ref = xn[:, :, None] + (shift - xn)[:, :, None] * coef.double()
+    assert float((out.cpu().double() - ref).abs().max()) < 1e-5 * float(
+        ref.abs().max())
+    assert float((new_prev.cpu().double() - xn[:, -1]).abs().max()) < 1e-5 * float(
+        xn.abs().max())
+
+
 def test_lora_kernel_matches_matmul():
     g = torch.Generator().manual_seed(1)
     ranks = [96, 96, 64, 256]
