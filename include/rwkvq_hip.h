@@ -182,7 +182,7 @@ int rwkvq_layer_norm(const float* x, const float* w, const float* b, float* y,
  * out[(b*T+t), c, :] = xn + (shift - xn) * coef[c, :], shift = xn of the
  * previous token or prev[b] (zeros if prev is NULL) at t = 0;
  * new_prev[b] = xn of the last token (may be NULL).  ncoef is 1 or 6;
- * D <= 4096.
+ * D <= 4096 and a multiple of 4.
  * Replaces: _token_shift_stateful + the six lerps of the time mix and the
  * one of the channel mix (reference: quant_model.py:292-301, 643-650,
  * 803-809). */

@@ -89,6 +89,44 @@ layer_norm_k(const float* x, const float* __restrict__ w,
   }
 }
 
+// Row held as float4s: thread t owns columns 4 (t + 256 e) .. +3, e <
+// kMaxE4 (D <= 4096, D % 4 == 0) -- a quarter of the load and store
+// instructions of the scalar layout, which matters when one workgroup
+// carries a whole decode row.
+constexpr int kMaxE4 = 4;
+
+__device__ __forceinline__ void load_row4(const float* row, int D,
+                                          float4 (&v)[kMaxE4]) {
+#pragma unroll
+  for (int e = 0; e < kMaxE4; ++e) {
+    const int c = 4 * (threadIdx.x + e * kRowThreads);
+    v[e] = c < D ? *reinterpret_cast<const float4*>(row + c)
+                 : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+}
+
+// Mean and rstd of a float4 register row (two-pass, as the reference).
+__device__ __forceinline__ void row_stats4(const float4 (&v)[kMaxE4], int D,
+                                           float eps, float* sh, float& mean,
+                                           float& rstd) {
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < kMaxE4; ++e) s += (v[e].x + v[e].y) + (v[e].z + v[e].w);
+  mean = block_sum(s, sh) / (float)D;
+  float q = 0.f;
+#pragma unroll
+  for (int e = 0; e < kMaxE4; ++e) {
+    const int c = 4 * (threadIdx.x + e * kRowThreads);
+    if (c < D) {
+      const float a = v[e].x - mean, b = v[e].y - mean, cc = v[e].z - mean,
+                  d = v[e].w - mean;
+      q += (a * a + b * b) + (cc * cc + d * d);
+    }
+  }
+  const float var = block_sum(q, sh) / (float)D;
+  rstd = 1.f / sqrtf(var + eps);
+}
+
 // LN + token shift + ncoef lerps for one token row (b, t):
 //   out[(b*T+t), k, :] = xn + (shift - xn) * coef[k, :]
 // shift = xn of (b, t-1), or prev[b] (zeros when prev is null) at t = 0.
@@ -103,40 +141,51 @@ shift_lerp_k(const float* __restrict__ x, const float* __restrict__ lw,
   const int row = blockIdx.x;           // b * T + t
   const int t = row % T, bb = row / T;
   const float* xr = x + (size_t)row * D;
-  float v[kMaxE], pv[kMaxE];
-  load_row(xr, D, v);
-  if (t > 0) load_row(xr - D, D, pv);
-  else if (prev) load_row(prev + (size_t)bb * D, D, pv);
+  float4 v[kMaxE4], pv[kMaxE4];
+  load_row4(xr, D, v);
+  if (t > 0) load_row4(xr - D, D, pv);
+  else if (prev) load_row4(prev + (size_t)bb * D, D, pv);
   // every load is issued before the first store: on this target the
   // vector-memory counter covers stores too, so a load placed after a
   // store would also wait for that store
-  float cw[kMaxE], cb[kMaxE], cf[NC][kMaxE];
+  float4 cw[kMaxE4], cb[kMaxE4], cf[NC][kMaxE4];
+  load_row4(lw, D, cw);
+  load_row4(lb, D, cb);
 #pragma unroll
-  for (int e = 0; e < kMaxE; ++e) {
-    const int c = threadIdx.x + e * kRowThreads;
-    const bool in = c < D;
-    cw[e] = in ? lw[c] : 0.f;
-    cb[e] = in ? lb[c] : 0.f;
-#pragma unroll
-    for (int k = 0; k < NC; ++k) cf[k][e] = in ? coef[(size_t)k * D + c] : 0.f;
-  }
+  for (int k = 0; k < NC; ++k) load_row4(coef + (size_t)k * D, D, cf[k]);
   float mean, rstd;
-  row_stats(v, D, 1e-5f, sh, mean, rstd);
+  row_stats4(v, D, 1e-5f, sh, mean, rstd);
   float pmean = 0.f, prstd = 0.f;
-  if (t > 0) row_stats(pv, D, 1e-5f, sh, pmean, prstd);
+  if (t > 0) row_stats4(pv, D, 1e-5f, sh, pmean, prstd);
+  auto lane4 = [&](const float4& f, int i) {
+    return i == 0 ? f.x : i == 1 ? f.y : i == 2 ? f.z : f.w;
+  };
 #pragma unroll
-  for (int e = 0; e < kMaxE; ++e) {
-    const int c = threadIdx.x + e * kRowThreads;
+  for (int e = 0; e < kMaxE4; ++e) {
+    const int c = 4 * (threadIdx.x + e * kRowThreads);
     if (c >= D) continue;
-    const float xn = (v[e] - mean) * rstd * cw[e] + cb[e];
-    float sv;
-    if (t > 0) sv = (pv[e] - pmean) * prstd * cw[e] + cb[e];
-    else sv = prev ? pv[e] : 0.f;
-    const float xx = sv - xn;
+    float xn[4], xx[4];
 #pragma unroll
-    for (int k = 0; k < NC; ++k)
-      out[((size_t)row * NC + k) * D + c] = xn + xx * cf[k][e];
-    if (t == T - 1 && new_prev) new_prev[(size_t)bb * D + c] = xn;
+    for (int i = 0; i < 4; ++i) {
+      const float w_ = lane4(cw[e], i), b_ = lane4(cb[e], i);
+      xn[i] = (lane4(v[e], i) - mean) * rstd * w_ + b_;
+      float sv;
+      if (t > 0) sv = (lane4(pv[e], i) - pmean) * prstd * w_ + b_;
+      else sv = prev ? lane4(pv[e], i) : 0.f;
+      xx[i] = sv - xn[i];
+    }
+#pragma unroll
+    for (int k = 0; k < NC; ++k) {
+      float4 o;
+      o.x = xn[0] + xx[0] * cf[k][e].x;
+      o.y = xn[1] + xx[1] * cf[k][e].y;
+      o.z = xn[2] + xx[2] * cf[k][e].z;
+      o.w = xn[3] + xx[3] * cf[k][e].w;
+      *reinterpret_cast<float4*>(out + ((size_t)row * NC + k) * D + c) = o;
+    }
+    if (t == T - 1 && new_prev)
+      *reinterpret_cast<float4*>(new_prev + (size_t)bb * D + c) =
+          make_float4(xn[0], xn[1], xn[2], xn[3]);
   }
 }
 
@@ -532,8 +581,8 @@ int rwkvq_shift_lerp(const float* x, const float* ln_w, const float* ln_b,
                      const float* prev, const float* coef, int ncoef,
                      float* out, float* new_prev, int B, int T, int D,
                      void* stream) {
-  if (B <= 0 || T <= 0 || D <= 0 || D > kRowThreads * kMaxE ||
-      (ncoef != 1 && ncoef != 6))
+  if (B <= 0 || T <= 0 || D <= 0 || D > 4 * kRowThreads * kMaxE4 ||
+      D % 4 || (ncoef != 1 && ncoef != 6))
     return RWKVQ_ERR_ARG;
   if (ncoef == 6)
     hipLaunchKernelGGL(shift_lerp_k<6>, dim3(B * T), dim3(kRowThreads), 0,
