@@ -426,6 +426,25 @@ wkv_decode_k(const float* __restrict__ rkv, const float* __restrict__ yw,
     float4 q = *reinterpret_cast<const float4*>(state_in + soff + c);
     S[c] = q.x; S[c + 1] = q.y; S[c + 2] = q.z; S[c + 3] = q.w;
   }
+  // per-channel inputs of wave 0, also loaded up front: none depends on
+  // the LoRA phase, so their round trip overlaps it
+  float r = 0.f, k = 0.f, v = 0.f, w0c = 0.f, a0c = 0.f, kkc = 0.f,
+        kac = 0.f, rkc = 0.f, lw = 0.f, lb = 0.f, vf = 0.f, ywe = 0.f,
+        yae = 0.f, yve = 0.f, gc = 0.f, v0c = 0.f;
+  if (tid < kHead) {
+    const int c = h * kHead + tid;
+    const size_t e = (size_t)bi * D + c;
+    r = rkv[(size_t)bi * 3 * D + c];
+    k = rkv[(size_t)bi * 3 * D + D + c];
+    v = rkv[(size_t)bi * 3 * D + 2 * D + c];
+    w0c = w0[c]; a0c = a0[c]; kkc = k_k[c]; kac = k_a[c]; rkc = r_k[c];
+    lw = lnw[c]; lb = lnb[c];
+    if (!layer0) {
+      vf = vfirst[e]; v0c = v0[c];
+      if (!LORA) yve = yv[e];
+    }
+    if (!LORA) { ywe = yw[e]; yae = ya[e]; gc = g[e]; }
+  }
   __shared__ float s_up[4][kHead];
   if constexpr (LORA) {
     // The four branches' down outputs of token bi, concatenated (w, a, v,
@@ -491,25 +510,21 @@ wkv_decode_k(const float* __restrict__ rkv, const float* __restrict__ yw,
                       : j == 2 ? acc[2] : acc[3];
     __syncthreads();
   }
-  float vp = 0.f, gc = 0.f, lw = 0.f, lb = 0.f;
+  float vp = 0.f;
   if (tid < kHead) {
     const int c = h * kHead + tid;
     const size_t e = (size_t)bi * D + c;
-    const float r = rkv[(size_t)bi * 3 * D + c];
-    const float k = rkv[(size_t)bi * 3 * D + D + c];
-    float v = rkv[(size_t)bi * 3 * D + 2 * D + c];
-    const float ywe = LORA ? s_up[0][tid] : yw[e];
-    const float yae = LORA ? s_up[1][tid] : ya[e];
-    const float wv = __expf(-0.606531f * sigm(ywe + w0[c]));
-    const float av = sigm(yae + a0[c]);
-    const float kkr = k * k_k[c];
+    if (LORA) {
+      ywe = s_up[0][tid]; yae = s_up[1][tid]; yve = s_up[2][tid];
+      gc = s_up[3][tid];
+    }
+    const float wv = __expf(-0.606531f * sigm(ywe + w0c));
+    const float av = sigm(yae + a0c);
+    const float kkr = k * kkc;
     const float kk = kkr / sqrtf(wave_sum_dpp(kkr * kkr) + 1e-12f);
-    const float kp = k * (1.f + (av - 1.f) * k_a[c]);
-    gc = LORA ? s_up[3][tid] : g[e];
-    lw = lnw[c]; lb = lnb[c];
-    const float rkc = r_k[c];
+    const float kp = k * (1.f + (av - 1.f) * kac);
     if (!layer0)
-      v = v + (vfirst[e] - v) * sigm((LORA ? s_up[2][tid] : yv[e]) + v0[c]);
+      v = v + (vf - v) * sigm(yve + v0c);
     else vfirst[e] = v;
     const float dp = wave_sum_dpp(r * kp * rkc);
     reinterpret_cast<float*>(s_w)[tid] = wv;
