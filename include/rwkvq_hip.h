@@ -261,7 +261,8 @@ int rwkvq_wkv7_decode_lora(const float* rkv, const float* const* h,
 
 /* Grouped dense-fp16 GEMV of up to 4 low-rank branches in one launch:
  * y_j[n, r] = epi_j( sum_c x_j[n * x_ld_j + c] * W_j[r, c] ), n < N <= 8.
- * in_j % 16 == 0 and in_j <= 512, or in_j in {2048, 2560}.
+ * in_j % 16 == 0 and in_j <= 512, or in_j in {2048, 2560} (then x_j
+ * 16-byte aligned and x_ld_j % 4 == 0).
  * Replaces: QuantTMix._lora down/up products (reference:
  * quant_model.py:462-526). */
 int rwkvq_lora_gemv(int n_jobs, const void* const* W, const float* const* x,

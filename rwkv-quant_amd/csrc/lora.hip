@@ -48,35 +48,40 @@ template <int PER>
 __device__ __forceinline__ void lora_wide(const LoraJob& jo, int N, int lw,
                                           int lane) {
   // 4 rows per wave, all their weight loads in flight at once; lane l owns
-  // fp16 pairs p = l + 64 q (q < PER / 2), so consecutive lanes read
-  // consecutive dwords of a row (coalesced 256 B per instruction)
-  constexpr int PW = PER / 2;
+  // the 8-column chunks l + 64 q (q < PER / 8), so consecutive lanes read
+  // consecutive 16 bytes of a row (1 KiB per instruction)
+  constexpr int PQ = PER / 8;
   float res[8][4];                             // stores deferred to the end
-  uint32_t wv[4][PW];
+  uint4 wv[4][PQ];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int row = min(lw * 4 + j, jo.rows - 1);
-    const uint32_t* wr =
-        reinterpret_cast<const uint32_t*>(jo.W + (size_t)row * jo.in);
+    const uint4* wr = reinterpret_cast<const uint4*>(jo.W + (size_t)row * jo.in);
 #pragma unroll
-    for (int q = 0; q < PW; ++q) wv[j][q] = wr[lane + 64 * q];
+    for (int q = 0; q < PQ; ++q) wv[j][q] = wr[lane + 64 * q];
   }
 #pragma unroll
   for (int n = 0; n < 8; ++n) {
     if (n >= N) break;
-    const float2* xp =
-        reinterpret_cast<const float2*>(jo.x + (size_t)n * jo.x_ld);
-    uint32_t xh[PW];
+    const float4* xp =
+        reinterpret_cast<const float4*>(jo.x + (size_t)n * jo.x_ld);
+    uint4 xh[PQ];
 #pragma unroll
-    for (int q = 0; q < PW; ++q) {
-      const float2 f = xp[lane + 64 * q];
-      xh[q] = pack_h2(f.x, f.y);
+    for (int q = 0; q < PQ; ++q) {
+      const float4 f0 = xp[2 * (lane + 64 * q)], f1 = xp[2 * (lane + 64 * q) + 1];
+      xh[q] = make_uint4(pack_h2(f0.x, f0.y), pack_h2(f0.z, f0.w),
+                         pack_h2(f1.x, f1.y), pack_h2(f1.z, f1.w));
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       float a = 0.f;
 #pragma unroll
-      for (int q = 0; q < PW; ++q) a = dot2(wv[j][q], xh[q], a);
+      for (int q = 0; q < PQ; ++q) {
+        a = dot2(wv[j][q].x, xh[q].x, a);
+        a = dot2(wv[j][q].y, xh[q].y, a);
+        a = dot2(wv[j][q].z, xh[q].z, a);
+        a = dot2(wv[j][q].w, xh[q].w, a);
+      }
       res[n][j] = wave_sum_dpp(a);
     }
   }
@@ -182,6 +187,7 @@ extern "C" int rwkvq_lora_gemv(int n_jobs, const void* const* W,
     const bool wide = in[q] == 64 * 32 || in[q] == 64 * 40;
     if (rows[q] <= 0 || in[q] <= 0 || in[q] % 16 ||
         (!wide && in[q] > 8 * kMaxPer) || x_ld[q] < in[q] ||
+        (wide && (((uintptr_t)x[q] & 15) || x_ld[q] % 4)) ||   // float4 x
         y_ld[q] < rows[q])
       return RWKVQ_ERR_ARG;
     LoraJob& j = J.j[q];
