@@ -259,6 +259,18 @@ int rwkvq_wkv7_decode_lora(const float* rkv, const float* const* h,
                            float* out, int B, int H, int head_size,
                            void* stream);
 
+/* Dense fp16 rows in up to 8 segments of one matrix w [sum rows, in], for
+ * 1..16 input rows, on the matrix cores: segment j (rows seg_rows[j], a
+ * multiple of 16) reads x[n * x_ld + j * in + c] and writes
+ * seg_y[j][n * seg_rows[j] + r] = epi_j(sum_c x . w), epi_j = 4-bit field
+ * j of seg_modes (RWKVQ_EPI_*).  in % 128 == 0.
+ * Replaces: the down products of QuantTMix._lora for a decode batch, all
+ * branches in one launch (reference: quant_model.py:462-526). */
+int rwkvq_gemv_f16_seg(const uint16_t* w, int nseg, const int* seg_rows,
+                       int in, const float* x, long x_ld,
+                       float* const* seg_y, int n, int seg_modes,
+                       void* stream);
+
 /* Grouped dense-fp16 GEMV of up to 4 low-rank branches in one launch:
  * y_j[n, r] = epi_j( sum_c x_j[n * x_ld_j + c] * W_j[r, c] ), n < N <= 8.
  * in_j % 16 == 0 and in_j <= 512, or in_j in {2048, 2560} (then x_j

@@ -46,6 +46,12 @@ struct GemvArgs {
   float* y;              // [N, rows]
   long x_ld;
   int rows, in, out_per, n_seg, ks, rg, rpw, mode, n;
+  // segment table (matrix-core kernel, rwkvq_gemv_f16_seg): segment j
+  // holds rows [seg_end[j-1], seg_end[j]), reads x at x + j * in and writes
+  // seg_y[j] [n, rows of j]; 0 segments = uniform out_per segments
+  int nseg_tab, seg_modes;
+  int seg_end[8];
+  float* seg_y[8];
 };
 
 // Convert one lane's 32 x values of group g into the format's 16 fp16
@@ -287,18 +293,33 @@ gemv_kernel(GemvArgs a) {
 template <int FMT, int RT, int NS, int KSMAX>
 __global__ void __launch_bounds__(64 * KSMAX)
 bgemv_kernel(GemvArgs a) {
+  using RawT = typename RawOf<FMT>::T;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int i = lane & 15, q = lane >> 4;
   const int ng = a.in >> 5, nsb = a.in >> 8;
   const int row0 = blockIdx.x * 16 * RT;
-  const int seg = row0 / a.out_per;
+  // segment of this tile: uniform out_per, or the table (constant-index
+  // reads and value selects only)
+  int seg = row0 / a.out_per, s_lo = 0;
+  float* s_y = a.y;
+  if (a.nseg_tab > 0) {
+    seg = 0;
+    s_y = a.seg_y[0];
+#pragma unroll
+    for (int j = 1; j < 8; ++j) {
+      const bool past = j < a.nseg_tab && row0 >= a.seg_end[j - 1];
+      seg = past ? j : seg;
+      s_lo = past ? a.seg_end[j - 1] : s_lo;
+      s_y = past ? a.seg_y[j] : s_y;
+    }
+  }
   const int gw = wave * a.rpw * 4;         // first group of the wave's slice
   const bool xon = i < a.n;
   const float* xr = a.x + (size_t)(xon ? i : 0) * a.x_ld +
                     (size_t)seg * a.in + q * 32;
 
-  auto load_w = [&](int g, Raw (&dst)[RT]) {
+  auto load_w = [&](int g, RawT (&dst)[RT]) {
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
       load_raw<FMT>(a, row0 + 16 * rt + i, ng, nsb, g, dst[rt]);
@@ -316,7 +337,7 @@ bgemv_kernel(GemvArgs a) {
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) acc[rt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  auto mma_step = [&](int st, Raw (&w_raw)[RT], float4 (&xv)[8]) {
+  auto mma_step = [&](int st, RawT (&w_raw)[RT], float4 (&xv)[8]) {
     half8_t bx[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -342,7 +363,7 @@ bgemv_kernel(GemvArgs a) {
 
   if (NS == 2) {
     // both steps' loads in flight at once
-    Raw wa[RT], wb[RT];
+    RawT wa[RT], wb[RT];
     float4 xa[8], xb[8];
     load_w(gw + q, wa);
     load_x(gw, xa);
@@ -357,7 +378,7 @@ bgemv_kernel(GemvArgs a) {
   } else if (NS > 2) {
     // straight-line: step s + 1 loads while step s multiplies, in two
     // register sets (compile-time indices, no copies)
-    Raw w2[2][RT];
+    RawT w2[2][RT];
     float4 x2[2][8];
     load_w(gw + q, w2[0]);
     load_x(gw, x2[0]);
@@ -374,7 +395,7 @@ bgemv_kernel(GemvArgs a) {
   } else {
     // any step count: the same two register sets in a loop.  Loads past
     // the slice's last step are clamped to it (L2 hits, never used).
-    Raw wa[RT], wb[RT];
+    RawT wa[RT], wb[RT];
     float4 xa[8], xb[8];
     const int last = a.rpw - 1;
     load_w(gw + q, wa);
@@ -403,6 +424,14 @@ bgemv_kernel(GemvArgs a) {
       red[(wave * RT + rt) * 256 + v * 64 + lane] = acc[rt][v];
   __syncthreads();
   constexpr int kRows = 16 * RT;
+  const int mode = a.mode == RWKVQ_EPI_PER_SEG ? (a.seg_modes >> (4 * seg)) & 15
+                                               : a.mode;
+  int seg_hi = a.rows;
+  if (a.nseg_tab > 0) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      seg_hi = j == seg ? a.seg_end[j] : seg_hi;
+  }
   for (int idx = threadIdx.x; idx < kRows * 16; idx += a.ks * 64) {
     const int n = idx / kRows, r = idx % kRows;   // rows fastest: coalesced
     if (n >= a.n) break;
@@ -411,8 +440,10 @@ bgemv_kernel(GemvArgs a) {
     for (int k = 0; k < a.ks; ++k) v += red[k * RT * 256 + e];
     const int row = row0 + r;
     if (FMT == F_RTN8) v *= f16_bits_to_f32(a.d[row]);
-    float* yp = a.y + (size_t)n * a.rows + row;
-    switch (a.mode) {
+    float* yp = a.nseg_tab > 0
+                    ? s_y + (size_t)n * (seg_hi - s_lo) + (row - s_lo)
+                    : a.y + (size_t)n * a.rows + row;
+    switch (mode) {
       case RWKVQ_EPI_ADD: v += *yp; break;
       case RWKVQ_EPI_RELU2: v = v > 0.f ? v * v : 0.f; break;
       case RWKVQ_EPI_TANH: v = tanhf(v); break;
@@ -599,6 +630,33 @@ int rwkvq_gemv_rtn8(const int8_t* codes, const uint16_t* scale, int rows,
   a.x_ld = x_ld > 0 ? x_ld : (long)a.n_seg * in;
   if (a.x_ld < (long)a.n_seg * in) return RWKVQ_ERR_ARG;
   return launch_fmt<F_RTN8>(a, (hipStream_t)stream);
+}
+
+int rwkvq_gemv_f16_seg(const uint16_t* w, int nseg, const int* seg_rows,
+                       int in, const float* x, long x_ld,
+                       float* const* seg_y, int n, int seg_modes,
+                       void* stream) {
+  if (!w || !x || nseg < 1 || nseg > 8 || in <= 0 || in % 128 || n < 1 ||
+      n > 16)
+    return RWKVQ_ERR_ARG;
+  GemvArgs a{};
+  int rows = 0;
+  for (int j = 0; j < nseg; ++j) {
+    const int m = (seg_modes >> (4 * j)) & 15;
+    if (seg_rows[j] <= 0 || seg_rows[j] % 16 || !seg_y[j] ||
+        m > RWKVQ_EPI_SIGMOID)
+      return RWKVQ_ERR_ARG;
+    rows += seg_rows[j];
+    a.seg_end[j] = rows;
+    a.seg_y[j] = seg_y[j];
+  }
+  a.q = reinterpret_cast<const uint8_t*>(w);
+  a.x = x; a.y = seg_y[0];
+  a.rows = rows; a.in = in; a.out_per = 16; a.n_seg = nseg; a.n = n;
+  a.nseg_tab = nseg; a.mode = RWKVQ_EPI_PER_SEG; a.seg_modes = seg_modes;
+  a.x_ld = x_ld > 0 ? x_ld : (long)nseg * in;
+  if (a.x_ld < (long)nseg * in) return RWKVQ_ERR_ARG;
+  return launch_bg<F_F16>(a, (hipStream_t)stream);
 }
 
 }  // extern "C"

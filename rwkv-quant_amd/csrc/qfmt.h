@@ -68,6 +68,22 @@ __device__ __forceinline__ void load_raw(const Args& a, int row, int ng,
   }
 }
 
+// Dense fp16 rows (F_F16): one lane's 32-column group is 64 bytes, held
+// as loaded; the pair order is the natural one.
+struct RawF16 {
+  uint4 q[4];
+};
+template <int FMT> struct RawOf { using T = Raw; };
+template <> struct RawOf<F_F16> { using T = RawF16; };
+
+template <int FMT, class Args>
+__device__ __forceinline__ void load_raw(const Args& a, int row, int ng,
+                                         int nsb, int g, RawF16& r) {
+  const uint8_t* p = a.q + ((size_t)row * a.in + g * 32) * 2;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r.q[i] = ld16(p + 16 * i);
+}
+
 // Pin the fields of a Raw that the format loads (pinning an unused one
 // would keep its registers alive).
 template <int FMT>
@@ -165,6 +181,17 @@ __device__ __forceinline__ void dequant_group(const Raw& r, int kb,
     const h2_t bias = {(_Float16)1152.f, (_Float16)1152.f};
 #pragma unroll
     for (int i = 0; i < 16; ++i) w[i] = h2_bits(as_h2(w[i]) - bias);
+  }
+}
+
+// Dense fp16 rows: the stored values are the weights.
+template <int FMT>
+__device__ __forceinline__ void dequant_group(const RawF16& r, int,
+                                              uint32_t w[16]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    w[4 * i] = r.q[i].x; w[4 * i + 1] = r.q[i].y;
+    w[4 * i + 2] = r.q[i].z; w[4 * i + 3] = r.q[i].w;
   }
 }
 

@@ -45,6 +45,8 @@ FUSE = True
 FUSE_DECODE = True
 USE_GRAPH = True
 LORA_KERNEL_MAX_N = 8          # rows handled by the grouped LoRA kernel
+DOWN_SEG_MIN_N = 3             # decode rows from which the LoRA down
+                               # products take the segmented MFMA GEMV
 
 _LORA = ("w1", "w2", "a1", "a2", "v1", "v2", "g1", "g2")
 
@@ -205,6 +207,19 @@ class QuantTMix:
             A = lora(b + "1", False).to(torch.float16).contiguous()
             Bm = lora(b + "2", True).to(torch.float16).contiguous()
             self.lora[b] = (A, Bm)
+        # the down factors stacked in lerp-slot order (v, w, a, g) in one
+        # buffer (the per-branch A are views of it): one segmented launch
+        # runs all down products of a decode batch
+        self.down_order = [b for b in ("v", "w", "a", "g") if b in self.lora]
+        A_cat = torch.cat([self.lora[b][0] for b in self.down_order]).contiguous()
+        off = 0
+        for b in self.down_order:
+            r = self.lora[b][0].shape[0]
+            self.lora[b] = (A_cat[off:off + r], self.lora[b][1])
+            off += r
+        self.down_cat = A_cat
+        self.down_seg_ok = A_cat.shape[1] % 128 == 0 and all(
+            self.lora[b][0].shape[0] % 16 == 0 for b in self.down_order)
         self.rkv_fused = None
         lins = [self.r_proj, self.k_proj, self.v_proj]
         if all(isinstance(l, GwQuantLinear) for l in lins) and \
@@ -230,12 +245,7 @@ class QuantTMix:
         N, C = wk.N, self.C
         branches = list(self.lora)
         if N <= LORA_KERNEL_MAX_N:
-            xs_flat = wk.xs.view(N, 6 * C)
-            W = [self.lora[b][0] for b in branches]
-            X = [xs_flat[:, self.SLOT[b] * C:] for b in branches]
-            self._grouped(W, X, [6 * C] * len(branches),
-                          [wk.h[b] for b in branches],
-                          [self.EPI_DOWN[b] for b in branches], N)
+            self.run_lora_down(wk)
             W = [self.lora[b][1] for b in branches]
             X = [wk.h[b] for b in branches]
             self._grouped(W, X, [wk.h[b].shape[1] for b in branches],
@@ -288,10 +298,25 @@ class QuantTMix:
     def run_lora_down(self, wk):
         """The down products only (decode with the up products folded into
         the WKV step): one launch, results (after tanh / sigmoid) in
-        wk.h[b]."""
+        wk.h[b].  Three or more rows: the segmented matrix-core GEMV over
+        the stacked factors; fewer: the grouped lane-dot kernel."""
         N, C = wk.N, self.C
-        br = list(self.lora)
         xs_flat = wk.xs.view(N, 6 * C)
+        if N >= DOWN_SEG_MIN_N and self.down_seg_ok and N <= 16:
+            order = self.down_order
+            rows = (ctypes.c_int * len(order))(
+                *[self.lora[b][0].shape[0] for b in order])
+            ys = (ctypes.c_void_p * len(order))(
+                *[wk.h[b].data_ptr() for b in order])
+            modes = 0
+            for j, b in enumerate(order):
+                modes |= self.EPI_DOWN[b] << (4 * j)
+            _lib.call("rwkvq_gemv_f16_seg", _lib.ptr(self.down_cat),
+                      len(order), rows, C,
+                      _lib.ptr(xs_flat[:, self.SLOT[order[0]] * C:]), 6 * C,
+                      ys, N, modes, _stream())
+            return
+        br = list(self.lora)
         self._grouped([self.lora[b][0] for b in br],
                       [xs_flat[:, self.SLOT[b] * C:] for b in br],
                       [6 * C] * len(br), [wk.h[b] for b in br],

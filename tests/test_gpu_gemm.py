@@ -159,3 +159,46 @@ def test_gemm_f16_per_segment_epilogue():
         ref = f(xs[:, 2 + j].half().float() @ W[j * R:(j + 1) * R].float().t())
         assert torch.allclose(y[:, j * R:(j + 1) * R], ref, rtol=1e-4,
                               atol=1e-5)
+
+
+@pytest.mark.parametrize("n", [1, 3, 8, 16])
+@pytest.mark.parametrize("ranks", [(64, 96, 96, 256), (96, 96, 256)])
+def test_gemv_f16_segments(n, ranks):
+    """The decode LoRA down products in one launch: segment j of the
+    stacked fp16 factors reads input slot j and writes its own output with
+    its own epilogue; against the float64 product of the fp16 operands."""
+    g = torch.Generator().manual_seed(n + len(ranks))
+    K = 2048
+    A = [(torch.randn(r, K, generator=g) * 0.05).half() for r in ranks]
+    xs = torch.randn(n, 6, K, generator=g)
+    modes = [_lib.EPI_STORE, _lib.EPI_TANH, _lib.EPI_STORE, _lib.EPI_SIGMOID]
+    modes = modes[-len(ranks):]
+    fns = {_lib.EPI_STORE: lambda v: v, _lib.EPI_TANH: np.tanh,
+           _lib.EPI_SIGMOID: lambda v: 1 / (1 + np.exp(-v))}
+    Ad = torch.cat(A).cuda()
+    xd = xs.cuda()
+    ys = [torch.empty(n, r, device="cuda") for r in ranks]
+    import ctypes
+    rows = (ctypes.c_int * len(ranks))(*ranks)
+    yp = (ctypes.c_void_p * len(ranks))(*[y.data_ptr() for y in ys])
+    sm = sum(m << (4 * j) for j, m in enumerate(modes))
+    s0 = 6 - len(ranks)
+    _lib.call("rwkvq_gemv_f16_seg", _lib.ptr(Ad), len(ranks), rows, K,
+              _lib.ptr(xd[:, s0]), 6 * K, yp, n, sm, _lib.stream_handle())
+    for j, (Aj, m) in enumerate(zip(A, modes)):
+        ref = fns[m](xs[:, s0 + j].half().double().numpy()
+                     @ Aj.double().numpy().T)
+        assert relmax(ys[j].cpu().numpy(), ref) < 2e-5, j
+
+
+def test_gemv_f16_segments_errors():
+    A = torch.zeros(96, 2048, dtype=torch.float16, device="cuda")
+    x = torch.zeros(17, 2048, device="cuda")
+    y = torch.empty(17, 96, device="cuda")
+    import ctypes
+    yp = (ctypes.c_void_p * 1)(y.data_ptr())
+    for rows, n in ((90, 4), (96, 17), (96, 0)):
+        r = (ctypes.c_int * 1)(rows)
+        with pytest.raises(_lib.HipKernelError):
+            _lib.call("rwkvq_gemv_f16_seg", _lib.ptr(A), 1, r, 2048,
+                      _lib.ptr(x), 2048, yp, n, 0, _lib.stream_handle())
