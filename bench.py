@@ -227,16 +227,17 @@ def trace_summary(path, top=40):
               f"{mn / 1e3:8.2f} {mx / 1e3:8.2f} {100 * tot / total:5.1f}%")
 
 
-def decode_bench(preset, batches, n_tok, dev):
-    """ms per decode step of the 1.5B-shaped model (graph replay, state
-    carried between steps, fresh uniform-random token ids each step)."""
+def decode_bench(preset, batches, n_tok, dev, shape="1.5b"):
+    """ms per decode step of the 1.5B- (or 2.9B-) shaped model (graph
+    replay, state carried between steps, fresh uniform-random token ids
+    each step)."""
     import torch
     from rwkv_quant.backends.hip.quant_model import QuantRWKV7
     from rwkv_quant.models.synthetic import SHAPES as MS, quantized_model
     t0 = time.time()
     ck = quantized_model(preset, seed=0, device=dev, **{
-        k: v for k, v in MS["1.5b"].items() if k != "vocab"},
-        vocab=MS["1.5b"]["vocab"])
+        k: v for k, v in MS[shape].items() if k != "vocab"},
+        vocab=MS[shape]["vocab"])
     model = QuantRWKV7(ck, device=dev)
     del ck
     build_s = time.time() - t0
@@ -333,11 +334,23 @@ def pmc_pass(args, dev):
           f"{per}", flush=True)
 
 
-def pp512(model, dev):
-    """pp512 with the projection FLOP rate (2 * 1.39e9 weight elements
-    of the 1.5B shape per token, head included)."""
-    pf = prefill_bench(model, 512, dev)
-    flop = 2 * 1_392_246_784 * 512
+def weight_elems(shape):
+    """Matmul weight elements one token meets in the forward of the shape:
+    r/k/v/o, channel-mix key/value, the LoRA factors (no v branch in layer
+    0) and the head (1.39e9 for 1.5B, 2.78e9 for 2.9B)."""
+    from rwkv_quant.models.synthetic import SHAPES as MS, lora_ranks
+    sh = MS[shape]
+    D, F, L = sh["n_embd"], sh["ffn"], sh["n_layer"]
+    rk = lora_ranks(D)
+    per = 4 * D * D + 2 * D * F + 2 * D * sum(rk.values())
+    return L * per - 2 * D * rk["v"] + sh["vocab"] * D
+
+
+def pp512(model, dev, T=512, shape="1.5b"):
+    """Prefill of T tokens with the projection FLOP rate
+    (2 * weight_elems(shape) per token)."""
+    pf = prefill_bench(model, T, dev)
+    flop = 2 * weight_elems(shape) * T
     pf["tflop_s"] = round(flop / (pf["ms"] * 1e-3) / 1e12, 2)
     return pf
 
@@ -352,11 +365,15 @@ def main():
     ap.add_argument("--no-model", action="store_true",
                     help="skip the 1.5B decode / pp512 measurements")
     ap.add_argument("--decode-tokens", type=int, default=128)
-    ap.add_argument("--only", choices=("decode", "prefill"), default=None,
+    ap.add_argument("--only", choices=("decode", "prefill", "decode2.9b",
+                                       "prefill2.9b"), default=None,
                     help="run one model workload alone (for a per-workload "
                          "rocprofv3 profile); prints that section only")
-    ap.add_argument("--decode-batches", default="1,8",
-                    help="decode batch sizes for --only decode")
+    ap.add_argument("--decode-batches", default=None,
+                    help="decode batch sizes for --only decode (default 1,8; "
+                         "1,32 for decode2.9b)")
+    ap.add_argument("--no-2p9b", action="store_true",
+                    help="skip the 2.9B decode / pp2048 measurements")
     ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
                     help="print the per-kernel table of a rocprofv3 kernel "
                          "trace after its last marker kernel and exit")
@@ -380,15 +397,24 @@ def main():
     if args.pmc_pass:
         pmc_pass(args, dev)
         return
-    if args.only == "decode":
-        bs = tuple(int(b) for b in args.decode_batches.split(","))
-        _, dec = decode_bench("compression", bs, args.decode_tokens, dev)
-        print(json.dumps({"decode_1p5b_compression": dec}), flush=True)
+    if args.only in ("decode", "decode2.9b"):
+        big = args.only == "decode2.9b"
+        bs = tuple(int(b) for b in (args.decode_batches or (
+            "1,32" if big else "1,8")).split(","))
+        _, dec = decode_bench("compression", bs, args.decode_tokens, dev,
+                              "2.9b" if big else "1.5b")
+        key = "decode_2p9b_compression" if big else "decode_1p5b_compression"
+        print(json.dumps({key: dec}), flush=True)
         return
     if args.only == "prefill":
         model, _ = decode_bench("reduction", (), 0, dev)
         print(json.dumps({"pp512_1p5b_reduction":
                           pp512(model, dev)}), flush=True)
+        return
+    if args.only == "prefill2.9b":
+        model, _ = decode_bench("reduction", (), 0, dev, "2.9b")
+        print(json.dumps({"pp2048_2p9b_reduction":
+                          pp512(model, dev, 2048, "2.9b")}), flush=True)
         return
     qts = build_set()
     per = algorithmic_bytes(qts)
@@ -434,6 +460,17 @@ def main():
         model, dec_r = decode_bench("reduction", (1,), 32, dev)
         out["decode_1p5b_reduction"] = dec_r
         out["pp512_1p5b_reduction"] = pp512(model, dev)
+        del model
+        torch.cuda.empty_cache()
+    if not args.no_model and not args.no_2p9b:
+        # 2.9B shape, decode at batch 1 and 32, prefill T=2048
+        model, dec = decode_bench("compression", (1, 32), 64, dev, "2.9b")
+        out["decode_2p9b_compression"] = dec
+        del model
+        torch.cuda.empty_cache()
+        model, dec_r = decode_bench("reduction", (1,), 32, dev, "2.9b")
+        out["decode_2p9b_reduction"] = dec_r
+        out["pp2048_2p9b_reduction"] = pp512(model, dev, 2048, "2.9b")
         del model
         torch.cuda.empty_cache()
     if not args.no_cpu:
