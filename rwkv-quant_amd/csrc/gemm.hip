@@ -155,16 +155,21 @@ __device__ __forceinline__ void weights_of(const Raw2& r2, int gi, int kb,
   }
 }
 
-template <int FMT, int WN, int WM>
-__global__ void __launch_bounds__(256)
+template <int FMT, int WN, int WM, int KG>
+__global__ void __launch_bounds__(256 * KG)
 gemm_kernel(GemmArgs a) {
   constexpr int BM = 32 * WM;
   constexpr int BN = 128 * WN;
   constexpr int XI = BM * 16 / 256;          // staging items per thread
-  __shared__ __attribute__((aligned(16))) _Float16 sx[2][BM * kRowH];
+  // KG groups of 4 waves share the tile and split its K steps (group g
+  // takes steps g, g + KG, ...): KG waves per SIMD hide each other's
+  // latency without a smaller tile; the groups' sums meet in LDS at the end
+  __shared__ __attribute__((aligned(16))) _Float16 sx[KG][2][BM * kRowH];
 
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wave_all = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int kg = wave_all >> 2, wave = wave_all & 3;
+  const int tid = threadIdx.x & 255;         // thread index in the group
   const int r = lane & 31, h = lane >> 5;
   // Tile order: workgroup b runs on XCD b % 8 (round-robin dispatch).  The
   // M tiles of one N tile go to the same XCD back to back, so that XCD's L2
@@ -191,7 +196,7 @@ gemm_kernel(GemmArgs a) {
   auto load_x = [&](int c) {
 #pragma unroll
     for (int p = 0; p < XI; ++p) {
-      const int it = threadIdx.x + 256 * p;
+      const int it = tid + 256 * p;
       const int t = min(m0 + (it >> 4), a.M - 1);
       const int gq = (it >> 2) & 3, s = it & 3;
       int ca, cb;
@@ -204,9 +209,9 @@ gemm_kernel(GemmArgs a) {
   auto store_x = [&](int buf) {
 #pragma unroll
     for (int p = 0; p < XI; ++p) {
-      const int it = threadIdx.x + 256 * p;
+      const int it = tid + 256 * p;
       const int tl = it >> 4, gq = (it >> 2) & 3, s = it & 3;
-      *reinterpret_cast<uint4*>(&sx[buf][tl * kRowH + gq * 32 + s * 8]) =
+      *reinterpret_cast<uint4*>(&sx[kg][buf][tl * kRowH + gq * 32 + s * 8]) =
           x_pairs<FMT>(xa[p], xbv[p]);
     }
   };
@@ -231,19 +236,22 @@ gemm_kernel(GemmArgs a) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[mi][ni][v] = 0.f;
 
-  load_w(0, cur);
-  load_x(0);
+  load_w(kg, cur);
+  load_x(kg);
   store_x(0);
   __syncthreads();
 
-  for (int c = 0; c < nsteps; ++c) {
-    const int cn = min(c + 1, nsteps - 1);     // clamped: loads stay in W / x
+  const int nsg = nsteps / KG;                 // steps of each group
+  for (int i = 0; i < nsg; ++i) {
+    const int c = i * KG + kg;
+    // clamped to the group's last step: loads stay in W / x
+    const int cn = min(c + KG, nsteps - KG + kg);
     load_w(cn, nxt);
     load_x(cn);
-    // keep the loads of step c + 1 ahead of this step's MFMAs: left to
+    // keep the loads of step c + KG ahead of this step's MFMAs: left to
     // itself the scheduler sinks them next to their use
     __builtin_amdgcn_sched_barrier(0);
-    const _Float16* xs = sx[c & 1];
+    const _Float16* xs = sx[kg][i & 1];
 #pragma unroll
     for (int gi = 0; gi < 2; ++gi) {
       uint32_t w[WN][16];
@@ -275,10 +283,38 @@ gemm_kernel(GemmArgs a) {
     for (int p = 0; p < XI; ++p) { pin(xa[p]); pin(xbv[p]); }
 #pragma unroll
     for (int ni = 0; ni < WN; ++ni) pin_raw2<FMT>(nxt[ni]);
-    store_x((c + 1) & 1);
+    store_x((i + 1) & 1);
     __syncthreads();
 #pragma unroll
     for (int ni = 0; ni < WN; ++ni) cur[ni] = nxt[ni];
+  }
+
+  if constexpr (KG > 1) {
+    // group 1 hands its sums to group 0 through the x buffers (free: the
+    // loop ended on a barrier); 4 waves x 16 WM WN floats x 64 lanes
+    // fits them for every tile of this kernel
+    constexpr int NA = WM * WN * 16;
+    static_assert(4 * NA * 64 * 4 <= (int)sizeof(sx), "reduction buffer");
+    float* red = reinterpret_cast<float*>(&sx[0][0][0]);
+    if (kg == 1) {
+#pragma unroll
+      for (int mi = 0; mi < WM; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < WN; ++ni)
+#pragma unroll
+          for (int v = 0; v < 16; ++v)
+            red[(wave * NA + (mi * WN + ni) * 16 + v) * 64 + lane] =
+                acc[mi][ni][v];
+    }
+    __syncthreads();
+    if (kg == 1) return;
+#pragma unroll
+    for (int mi = 0; mi < WM; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < WN; ++ni)
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          acc[mi][ni][v] += red[(wave * NA + (mi * WN + ni) * 16 + v) * 64 + lane];
   }
 
   // ---- epilogue: lane holds tokens m0 + 32 mi + r, rows 4 at a time
@@ -328,13 +364,24 @@ gemm_kernel(GemmArgs a) {
   }
 }
 
+#ifndef RWKVQ_GEMM_KG
+#define RWKVQ_GEMM_KG 2
+#endif
+
+// Two K groups (8 waves) wherever the tile's registers allow two waves per
+// SIMD (all tiles but 256 x 128) and the step count is even.
 template <int FMT, int WN, int WM>
 int launch_tile(const GemmArgs& a, hipStream_t s) {
   GemmArgs b = a;
   b.nt = a.N / (128 * WN);
   b.mt = (a.M + 32 * WM - 1) / (32 * WM);
-  hipLaunchKernelGGL((gemm_kernel<FMT, WN, WM>), dim3(b.nt * b.mt),
-                     dim3(256), 0, s, b);
+  constexpr bool two = RWKVQ_GEMM_KG == 2 && WN * WM <= 4;
+  if (two && (a.in / kStepK) % 2 == 0)
+    hipLaunchKernelGGL((gemm_kernel<FMT, WN, WM, two ? 2 : 1>),
+                       dim3(b.nt * b.mt), dim3(512), 0, s, b);
+  else
+    hipLaunchKernelGGL((gemm_kernel<FMT, WN, WM, 1>), dim3(b.nt * b.mt),
+                       dim3(256), 0, s, b);
   return hipGetLastError() == hipSuccess ? RWKVQ_OK : RWKVQ_ERR_LAUNCH;
 }
 
