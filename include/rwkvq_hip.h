@@ -218,6 +218,23 @@ int rwkvq_wkv7_scan(const float* r, long r_ld, const float* w, const float* k,
                     long y_ld, int B, int T, int H, int head_size,
                     void* stream);
 
+/* rwkvq_wkv7_scan in 16-step chunks: per (sequence, head, chunk) the
+ * chunk's transition is built in parallel in WY form (S_end = S0 P +
+ * V^T Bq, Y = S0 Ry + V^T Yq, from the cumulative log decay and a 16 x 16
+ * unit triangular solve), then the chunks are applied in order on the
+ * fp32 matrix cores.  ws: device workspace of at least
+ * B * H * ceil(T / 16) * 6400 floats (ws_floats), 16-byte aligned; decays
+ * are floored at e^-60.  Same result as the step-by-step scan to fp32
+ * rounding (the float64 oracle bar, 1e-5 relative, holds for both).
+ * Replaces: rwkv_metal.wkv7_infer for T > 1 (reference: quant_model.py:
+ * 118-125, 714; math rwkv7_ref.py:236-255). */
+int rwkvq_wkv7_scan_chunked(const float* r, long r_ld, const float* w,
+                            const float* k, const float* v, const float* a,
+                            const float* b, long ld, const float* state_in,
+                            float* state_out, float* y, long y_ld, int B,
+                            int T, int H, int head_size, float* ws,
+                            long ws_floats, void* stream);
+
 /* Time-mix tail per head: out = ((GN(y) ln_w + ln_b) + (sum r k' r_k) v') g
  * with a two-pass group norm (eps 64e-5); r is rkv[:, 0, :].
  * Replaces: wkv_tail (reference: fused_tail.py:43-110) and the unfused

@@ -576,6 +576,292 @@ wkv_decode_k(const float* __restrict__ rkv, const float* __restrict__ yw,
   }
 }
 
+// ---------------------------------------------------------------------------
+// Chunked WKV-7 scan (prefill).  Per (sequence, head) the recurrence over a
+// chunk of L = 16 steps, s_t = s_{t-1} diag(w_t) + (s_{t-1}.a_t) b_t +
+// v_t k_t for every value row s (a vector over the key index), is linear in
+// the chunk's start state S0 and in its values V:
+//   S_end = S0 P + V^T Bq,   Y = S0 Ry + V^T Yq      (Y[i][t] = y_t[i])
+// With G[t] the cumulative log decay over the chunk (G[0] = 0), u_t =
+// s_{t-1}.a_t solves a unit triangular system, U (I - M^T) = S0 C + V N^T:
+//   C[k][t]  = e^{G[t]} a_t                  M[t][j] = b_j.(e^{G[t]-G[j+1]} a_t)
+//   N[t][j]  = k_j.(e^{G[t]-G[j+1]} a_t)     (j < t; W = (I - M^T)^-1)
+//   Bt[j][t] = b_j.(e^{G[t+1]-G[j+1]} r_t)   Kt[j][t] = k_j.(...r_t)   (j <= t)
+//   Bh[j]    = b_j e^{G[L]-G[j+1]}           Kh[j]    = k_j e^{G[L]-G[j+1]}
+//   P  = diag(e^{G[L]}) + C W Bh   Bq = N^T W Bh + Kh
+//   Ry = e^{G[t+1]} r_t + C W Bt   Yq = N^T W Bt + Kt
+// (the WY form of a product of diagonal-plus-rank-one transitions).  One
+// launch builds these operators for every chunk in parallel; a second walks
+// the chunks in order per 16 value rows: two 64-deep products per chunk on
+// the fp32 matrix cores instead of 16 dependent scalar steps.  A ragged last
+// chunk is padded with identity steps (w = 1, k = a = b = r = v = 0).
+constexpr int kCL = 16;                 // steps per chunk
+constexpr int kOpsFloats = 6400;        // operator floats per (b, h, chunk)
+constexpr int kPad = 68;                // LDS row stride (floats)
+
+typedef float f32x4c_t __attribute__((ext_vector_type(4)));
+
+// Operator block of one chunk, in the lane order the scan kernel's fp32
+// MFMA (16x16x4: lane l holds A[l%16][l/16], B[l/16][l%16]) reads:
+//   [0, 4096)     Pf [w][l][s]  = P[4s + l/16][16w + l%16]      s < 16
+//   [4096, 5120)  Bqf[w][l][s]  = Bq[4s + l/16][16w + l%16]     s < 4
+//   [5120, 6144)  Ryf[w][l][s]  = Ry[16w + 4s + l/16][l%16]     s < 4
+//   [6144, 6400)  Yqf[l][s]     = Yq[4s + l/16][l%16]           s < 4
+__global__ void __launch_bounds__(256)
+wkv_chunk_ops_k(const float* __restrict__ r, long r_ld,
+                const float* __restrict__ w, const float* __restrict__ k,
+                const float* __restrict__ a, const float* __restrict__ b,
+                long ld, float* __restrict__ ops, int T, int H, int NC) {
+  const int c = blockIdx.x % NC, bh = blockIdx.x / NC;
+  const int h = bh % H, bi = bh / H;
+  const int tid = threadIdx.x;
+  __shared__ float sLw[kCL][kPad], sK[kCL][kPad], sA[kCL][kPad],
+      sB[kCL][kPad], sR[kCL][kPad], sG[kCL + 1][kPad];
+  __shared__ float sM[kCL][kCL + 1], sN[kCL][kCL + 1], sBt[kCL][kCL + 1],
+      sKt[kCL][kCL + 1], sW[kCL][kCL + 1], sNW[kCL][kCL + 1];
+  __shared__ float sCW[kHead][kCL + 1], sBh[kCL][kPad], sKh[kCL][kPad];
+
+  // 1. the chunk's inputs (identity steps past T); log decay floored at
+  //    -60 so that a decay of exactly 0 stays finite
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int idx = tid + 256 * e, t = idx >> 6, kap = idx & 63;
+    const int tg = c * kCL + t;
+    float wv = 1.f, kv = 0.f, av = 0.f, bv = 0.f, rv = 0.f;
+    if (tg < T) {
+      const size_t row = (size_t)bi * T + tg, col = (size_t)h * kHead + kap;
+      wv = w[row * ld + col]; kv = k[row * ld + col];
+      av = a[row * ld + col]; bv = b[row * ld + col];
+      rv = r[row * r_ld + col];
+    }
+    sLw[t][kap] = fmaxf(logf(wv), -60.f);
+    sK[t][kap] = kv; sA[t][kap] = av; sB[t][kap] = bv; sR[t][kap] = rv;
+  }
+  __syncthreads();
+  // 2. cumulative log decay per key channel
+  if (tid < kHead) {
+    float g = 0.f;
+    sG[0][tid] = 0.f;
+#pragma unroll
+    for (int t = 0; t < kCL; ++t) {
+      g += sLw[t][tid];
+      sG[t + 1][tid] = g;
+    }
+  }
+  __syncthreads();
+  // 3. the L x L products (thread = (t, j)) and Bh, Kh
+  {
+    const int t = tid >> 4, j = tid & 15;
+    float m = 0.f, n = 0.f, bt = 0.f, kt = 0.f;
+    for (int kap = 0; kap < kHead; ++kap) {
+      const float gj = sG[j + 1][kap], bj = sB[j][kap], kj = sK[j][kap];
+      const float e1 = j < t ? __expf(sG[t][kap] - gj) * sA[t][kap] : 0.f;
+      const float e2 = j <= t ? __expf(sG[t + 1][kap] - gj) * sR[t][kap] : 0.f;
+      m += bj * e1; n += kj * e1;
+      bt += bj * e2; kt += kj * e2;
+    }
+    sM[t][j] = m; sN[t][j] = n; sBt[j][t] = bt; sKt[j][t] = kt;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int idx = tid + 256 * e, jj = idx >> 6, mu = idx & 63;
+      const float d = __expf(sG[kCL][mu] - sG[jj + 1][mu]);
+      sBh[jj][mu] = sB[jj][mu] * d;
+      sKh[jj][mu] = sK[jj][mu] * d;
+    }
+  }
+  __syncthreads();
+  // 4. W = (I - M^T)^-1 (unit upper triangular), one column per thread:
+  //    W[i][cc] = sum_{m > i} M[m][i] W[m][cc], W[cc][cc] = 1
+  if (tid < kCL) {
+    const int cc = tid;
+    float col[kCL];
+#pragma unroll
+    for (int i = kCL - 1; i >= 0; --i) {
+      float sum = 0.f;
+#pragma unroll
+      for (int m2 = i + 1; m2 < kCL; ++m2) sum += sM[m2][i] * col[m2];
+      col[i] = i == cc ? 1.f : (i > cc ? 0.f : sum);
+    }
+#pragma unroll
+    for (int i = 0; i < kCL; ++i) sW[i][cc] = col[i];
+  }
+  __syncthreads();
+  // 5. CW = C W (thread = key channel x 4 columns), NW = N^T W
+  {
+    const int kap = tid >> 2, cq = tid & 3;
+    float cv[kCL];
+#pragma unroll
+    for (int t = 0; t < kCL; ++t) cv[t] = __expf(sG[t][kap]) * sA[t][kap];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int cc = cq * 4 + q;
+      float sum = 0.f;
+#pragma unroll
+      for (int t = 0; t < kCL; ++t) sum += cv[t] * sW[t][cc];
+      sCW[kap][cc] = sum;
+    }
+    const int j = tid >> 4, cc = tid & 15;
+    float sum = 0.f;
+#pragma unroll
+    for (int t = 0; t < kCL; ++t) sum += sN[t][j] * sW[t][cc];
+    sNW[j][cc] = sum;
+  }
+  __syncthreads();
+  // 6. the operators, written in the scan kernel's lane order
+  float* o = ops + ((size_t)bh * NC + c) * kOpsFloats;
+  for (int e = 0; e < 16; ++e) {
+    const int idx = tid + 256 * e;
+    const int s = idx & 15, l = (idx >> 4) & 63, wv = idx >> 10;
+    const int kap = 4 * s + (l >> 4), mu = 16 * wv + (l & 15);
+    float acc = kap == mu ? __expf(sG[kCL][kap]) : 0.f;
+#pragma unroll
+    for (int j = 0; j < kCL; ++j) acc += sCW[kap][j] * sBh[j][mu];
+    o[idx] = acc;
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int idx = tid + 256 * e;
+    const int s = idx & 3, l = (idx >> 2) & 63, wv = idx >> 8;
+    {
+      const int j = 4 * s + (l >> 4), mu = 16 * wv + (l & 15);
+      float acc = sKh[j][mu];
+#pragma unroll
+      for (int m2 = 0; m2 < kCL; ++m2) acc += sNW[j][m2] * sBh[m2][mu];
+      o[4096 + idx] = acc;
+    }
+    {
+      const int kap = 16 * wv + 4 * s + (l >> 4), t = l & 15;
+      float acc = __expf(sG[t + 1][kap]) * sR[t][kap];
+#pragma unroll
+      for (int j = 0; j < kCL; ++j) acc += sCW[kap][j] * sBt[j][t];
+      o[5120 + idx] = acc;
+    }
+  }
+  {
+    const int s = tid & 3, l = tid >> 2;
+    const int j = 4 * s + (l >> 4), t = l & 15;
+    float acc = sKt[j][t];
+#pragma unroll
+    for (int m2 = 0; m2 < kCL; ++m2) acc += sNW[j][m2] * sBt[m2][t];
+    o[6144 + tid] = acc;
+  }
+}
+
+// The sequential part: block = 16 value rows of one (sequence, head), 4
+// waves; per chunk wave w computes columns 16w..16w+15 of S0 P + V^T Bq and
+// key steps 16w..16w+15 of S0 Ry (wave 0 adds V^T Yq); the new rows and the
+// partial outputs meet in LDS.  The next chunk's operators and values are
+// loaded before the current chunk's products.
+__global__ void __launch_bounds__(256)
+wkv_chunk_scan_k(const float* __restrict__ v, long ld,
+                 const float* __restrict__ ops, const float* state_in,
+                 float* state_out, float* __restrict__ y, long y_ld, int T,
+                 int H, int NC) {
+  const int rb = blockIdx.x & 3, bh = blockIdx.x >> 2;
+  const int h = bh % H, bi = bh / H;
+  const int row0 = rb * 16;
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int li = lane & 15, lg = lane >> 4;
+  __shared__ __attribute__((aligned(16))) float sS[4][16][16];   // [k%4][row][k/4]
+  __shared__ float sY[4][4][64];                                // [wave][v][lane]
+
+  // A fragments of the rows: aS[s] = S[row0 + li][4 s + lg]
+  float aS[16];
+  {
+    const float* st = state_in + ((size_t)bh * kHead + row0 + li) * kHead;
+#pragma unroll
+    for (int s = 0; s < 16; ++s) aS[s] = st[4 * s + lg];
+  }
+  const float* opsb = ops + (size_t)bh * NC * kOpsFloats;
+  auto load_ops = [&](int c, float4 (&pf)[4], float4& bq, float4& ry,
+                      float4& yq, float (&vv)[4]) {
+    const float* o = opsb + (size_t)c * kOpsFloats;
+    const float4* p4 = reinterpret_cast<const float4*>(o + (wv * 64 + lane) * 16);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) pf[q] = p4[q];
+    bq = *reinterpret_cast<const float4*>(o + 4096 + (wv * 64 + lane) * 4);
+    ry = *reinterpret_cast<const float4*>(o + 5120 + (wv * 64 + lane) * 4);
+    yq = *reinterpret_cast<const float4*>(o + 6144 + lane * 4);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int tg = c * kCL + 4 * s + lg;
+      vv[s] = tg < T ? v[((size_t)bi * T + tg) * ld + (size_t)h * kHead + row0 + li]
+                     : 0.f;
+    }
+  };
+  float4 pf[4], bq, ry, yq, pf2[4], bq2, ry2, yq2;
+  float vv[4], vv2[4];
+  load_ops(0, pf, bq, ry, yq, vv);
+  for (int c = 0; c < NC; ++c) {
+    const int cn = min(c + 1, NC - 1);
+    load_ops(cn, pf2, bq2, ry2, yq2, vv2);
+    const float pfs[16] = {pf[0].x, pf[0].y, pf[0].z, pf[0].w, pf[1].x, pf[1].y,
+                           pf[1].z, pf[1].w, pf[2].x, pf[2].y, pf[2].z, pf[2].w,
+                           pf[3].x, pf[3].y, pf[3].z, pf[3].w};
+    const float bqs[4] = {bq.x, bq.y, bq.z, bq.w};
+    const float rys[4] = {ry.x, ry.y, ry.z, ry.w};
+    const float yqs[4] = {yq.x, yq.y, yq.z, yq.w};
+    f32x4c_t accS = {0.f, 0.f, 0.f, 0.f}, accY = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 16; ++s)
+      accS = __builtin_amdgcn_mfma_f32_16x16x4f32(aS[s], pfs[s], accS, 0, 0, 0);
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      accS = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[s], bqs[s], accS, 0, 0, 0);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const float av = wv == 0 ? aS[s] : wv == 1 ? aS[4 + s]
+                     : wv == 2 ? aS[8 + s] : aS[12 + s];
+      accY = __builtin_amdgcn_mfma_f32_16x16x4f32(av, rys[s], accY, 0, 0, 0);
+    }
+    if (wv == 0) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        accY = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[s], yqs[s], accY, 0, 0, 0);
+    }
+    // lane holds new S[4 lg + q][16 wv + li] and partial Y[4 lg + q][li]
+    {
+      const int kcol = 16 * wv + li;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        sS[kcol & 3][4 * lg + q][kcol >> 2] = accS[q];
+        sY[wv][q][lane] = accY[q];
+      }
+    }
+    __syncthreads();
+    {
+      const float4* a4 = reinterpret_cast<const float4*>(&sS[lg][li][0]);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float4 f = a4[q];
+        aS[4 * q] = f.x; aS[4 * q + 1] = f.y; aS[4 * q + 2] = f.z; aS[4 * q + 3] = f.w;
+      }
+      // output element (row i, step t) of this chunk: C layout lane
+      // t + 16 (i / 4), register i % 4
+      const int i = threadIdx.x & 15, t = threadIdx.x >> 4;
+      const int tg = c * kCL + t;
+      const int src = t + 16 * (i >> 2), q = i & 3;
+      const float yv = (sY[0][q][src] + sY[1][q][src]) + (sY[2][q][src] + sY[3][q][src]);
+      if (tg < T)
+        y[((size_t)bi * T + tg) * y_ld + (size_t)h * kHead + row0 + i] = yv;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < 4; ++q) pf[q] = pf2[q];
+    bq = bq2; ry = ry2; yq = yq2;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) vv[s] = vv2[s];
+  }
+  // final rows (aS holds them in A-fragment order; sS in [k%4][row][k/4])
+  float* so = state_out + ((size_t)bh * kHead + row0) * kHead;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int idx = threadIdx.x + 256 * e, rr = idx >> 6, kk = idx & 63;
+    so[(size_t)rr * kHead + kk] = sS[kk & 3][rr][kk >> 2];
+  }
+}
+
 inline int ok_launch() {
   return hipGetLastError() == hipSuccess ? RWKVQ_OK : RWKVQ_ERR_LAUNCH;
 }
@@ -637,6 +923,28 @@ int rwkvq_wkv7_scan(const float* r, long r_ld, const float* w, const float* k,
                      dim3(kScanThreads), 0, (hipStream_t)stream, r, r_ld, w,
                      k, v, a, b, ld, state_in ? state_in : state_out,
                      state_out, y, y_ld, T, H);
+  return ok_launch();
+}
+
+int rwkvq_wkv7_scan_chunked(const float* r, long r_ld, const float* w,
+                            const float* k, const float* v, const float* a,
+                            const float* b, long ld, const float* state_in,
+                            float* state_out, float* y, long y_ld, int B,
+                            int T, int H, int head_size, float* ws,
+                            long ws_floats, void* stream) {
+  if (B <= 0 || T <= 0 || H <= 0 || head_size != kHead || ld < H * kHead ||
+      r_ld < H * kHead || y_ld < H * kHead || !ws || !state_out)
+    return RWKVQ_ERR_ARG;
+  const int NC = (T + kCL - 1) / kCL;
+  if (ws_floats < (long)B * H * NC * kOpsFloats || ((uintptr_t)ws & 15))
+    return RWKVQ_ERR_ARG;
+  hipLaunchKernelGGL(wkv_chunk_ops_k, dim3(B * H * NC), dim3(256), 0,
+                     (hipStream_t)stream, r, r_ld, w, k, a, b, ld, ws, T, H,
+                     NC);
+  hipLaunchKernelGGL(wkv_chunk_scan_k, dim3(B * H * 4), dim3(256), 0,
+                     (hipStream_t)stream, v, ld, ws,
+                     state_in ? state_in : state_out, state_out, y, y_ld, T,
+                     H, NC);
   return ok_launch();
 }
 

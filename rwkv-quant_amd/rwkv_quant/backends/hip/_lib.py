@@ -49,6 +49,8 @@ SIGNATURES = {
                        _P, _P, _P, _I, _I, _I, _P],
     "rwkvq_wkv7_scan": [_P, _L, _P, _P, _P, _P, _P, _L, _P, _P, _P, _L, _I,
                         _I, _I, _I, _P],
+    "rwkvq_wkv7_scan_chunked": [_P, _L, _P, _P, _P, _P, _P, _L, _P, _P, _P,
+                                _L, _I, _I, _I, _I, _P, _L, _P],
     "rwkvq_wkv_tail": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P],
     "rwkvq_lora_gemv": [_I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P],
     "rwkvq_wkv7_decode_lora": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,

@@ -47,6 +47,10 @@ USE_GRAPH = True
 LORA_KERNEL_MAX_N = 8          # rows handled by the grouped LoRA kernel
 DOWN_SEG_MIN_N = 3             # decode rows from which the LoRA down
                                # products take the segmented MFMA GEMV
+WKV_CHUNK_MIN_T = 32           # sequence length from which the WKV scan
+                               # runs in 16-step chunks (operators + a
+                               # sequential pass on the matrix cores)
+WKV_CHUNK_OPS = 6400           # operator floats per (sequence, head, chunk)
 
 _LORA = ("w1", "w2", "a1", "a2", "v1", "v2", "g1", "g2")
 
@@ -517,7 +521,8 @@ class QuantRWKV7:
                   _lib.ptr(self.ln_out_b), _lib.ptr(wk.xo), N, C, 1e-5, st)
 
     def _wkv_seq(self, tm, wk, wkv_in, wkv_out, layer0, B, T, st):
-        """T > 1: per-channel inputs, chunked scan, tail (three launches)."""
+        """T > 1: per-channel inputs, the scan (step by step, or from
+        WKV_CHUNK_MIN_T on in 16-step chunks), tail."""
         N, C, H = B * T, self.n_embd, self.n_head
         _lib.call("rwkvq_wkv_prep", _lib.ptr(wk.rkv), _lib.ptr(wk.yl["w"]),
                   _lib.ptr(wk.yl["a"]),
@@ -526,10 +531,24 @@ class QuantRWKV7:
                   _lib.ptr(tm.k_a), _lib.ptr(wk.v_first), layer0,
                   _lib.ptr(wk.w), _lib.ptr(wk.kp), _lib.ptr(wk.vp),
                   _lib.ptr(wk.aa), _lib.ptr(wk.bb), N, C, self.head_size, st)
-        _lib.call("rwkvq_wkv7_scan", _lib.ptr(wk.rkv), 3 * C, _lib.ptr(wk.w),
-                  _lib.ptr(wk.kp), _lib.ptr(wk.vp), _lib.ptr(wk.aa),
-                  _lib.ptr(wk.bb), C, _lib.ptr(wkv_in), _lib.ptr(wkv_out),
-                  _lib.ptr(wk.y), C, B, T, H, self.head_size, st)
+        if T >= WKV_CHUNK_MIN_T:
+            need = B * H * (-(-T // 16)) * WKV_CHUNK_OPS
+            ops = getattr(wk, "wkv_ops", None)
+            if ops is None or ops.numel() < need:
+                # allocated by the warm-up run that precedes any capture
+                ops = wk.wkv_ops = torch.empty(need, dtype=torch.float32,
+                                               device=self.device)
+            _lib.call("rwkvq_wkv7_scan_chunked", _lib.ptr(wk.rkv), 3 * C,
+                      _lib.ptr(wk.w), _lib.ptr(wk.kp), _lib.ptr(wk.vp),
+                      _lib.ptr(wk.aa), _lib.ptr(wk.bb), C, _lib.ptr(wkv_in),
+                      _lib.ptr(wkv_out), _lib.ptr(wk.y), C, B, T, H,
+                      self.head_size, _lib.ptr(ops), ops.numel(), st)
+        else:
+            _lib.call("rwkvq_wkv7_scan", _lib.ptr(wk.rkv), 3 * C,
+                      _lib.ptr(wk.w), _lib.ptr(wk.kp), _lib.ptr(wk.vp),
+                      _lib.ptr(wk.aa), _lib.ptr(wk.bb), C, _lib.ptr(wkv_in),
+                      _lib.ptr(wkv_out), _lib.ptr(wk.y), C, B, T, H,
+                      self.head_size, st)
         _lib.call("rwkvq_wkv_tail", _lib.ptr(wk.y), _lib.ptr(wk.rkv),
                   _lib.ptr(wk.kp), _lib.ptr(wk.vp), _lib.ptr(wk.yl["g"]),
                   _lib.ptr(tm.r_k), _lib.ptr(tm.ln_x_w), _lib.ptr(tm.ln_x_b),

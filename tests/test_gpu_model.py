@@ -88,6 +88,68 @@ def test_shift_lerp_matches_float64(B, T, nc, prev):
         xn.abs().max())
 
 
+def _scan_chunked(dev, st_in, st_out, y, B, T, H):
+    D = H * 64
+    ws = torch.empty(B * H * (-(-T // 16)) * 6400, device="cuda")
+    _lib.call("rwkvq_wkv7_scan_chunked", _lib.ptr(dev[0]), D,
+              _lib.ptr(dev[1]), _lib.ptr(dev[2]), _lib.ptr(dev[3]),
+              _lib.ptr(dev[4]), _lib.ptr(dev[5]), D, _lib.ptr(st_in),
+              _lib.ptr(st_out), _lib.ptr(y), D, B, T, H, 64, _lib.ptr(ws),
+              ws.numel(), _lib.stream_handle())
+
+
+@pytest.mark.parametrize("B,T,H", [(1, 16, 4), (1, 37, 4), (2, 33, 8),
+                                   (1, 128, 32), (1, 512, 32)])
+def test_wkv7_scan_chunked_matches_oracle(B, T, H):
+    """The 16-step chunked scan (WY operators + fp32 matrix-core pass):
+    ragged last chunks, several sequences, the prefill length."""
+    print(f"wkv chunked B={B} T={T} H={H}", flush=True)
+    r, w, k, v, a, b, s0 = _wkv_inputs(B, T, H, seed=B * 1000 + T)
+    dev = [t.reshape(B, T, H * 64).contiguous().cuda()
+           for t in (r, w, k, v, a, b)]
+    st_in = s0.cuda().contiguous()
+    st_out = torch.empty_like(st_in)
+    y = torch.empty(B, T, H * 64, device="cuda")
+    _scan_chunked(dev, st_in, st_out, y, B, T, H)
+    yr, sr = wkv7(*(t.double().numpy() for t in (r, w, k, v, a, b)),
+                  s0.double().numpy())
+    yd = y.cpu().double().numpy().reshape(B, T, H, 64)
+    sd = st_out.cpu().double().numpy()
+    assert np.abs(yd - yr).max() / np.abs(yr).max() < 1e-5
+    assert np.abs(sd - sr).max() / np.abs(sr).max() < 1e-5
+    assert torch.equal(st_in.cpu(), s0)          # input state untouched
+
+
+def test_wkv7_scan_chunked_in_place_and_vs_steps():
+    """state_in == state_out (the model's own buffers may alias), and the
+    chunked and step-by-step scans agree to fp32 rounding; a zero decay
+    (floored at e^-60) stays finite."""
+    B, T, H = 1, 48, 8
+    r, w, k, v, a, b, s0 = _wkv_inputs(B, T, H, seed=77)
+    w[0, 5, 2, :7] = 0.0
+    dev = [t.reshape(B, T, H * 64).contiguous().cuda()
+           for t in (r, w, k, v, a, b)]
+    st = s0.cuda().contiguous()
+    y1 = torch.empty(B, T, H * 64, device="cuda")
+    _scan_chunked(dev, st, st, y1, B, T, H)
+    st2 = torch.empty_like(st)
+    y2 = torch.empty_like(y1)
+    D = H * 64
+    _lib.call("rwkvq_wkv7_scan", _lib.ptr(dev[0]), D, _lib.ptr(dev[1]),
+              _lib.ptr(dev[2]), _lib.ptr(dev[3]), _lib.ptr(dev[4]),
+              _lib.ptr(dev[5]), D, _lib.ptr(s0.cuda()), _lib.ptr(st2),
+              _lib.ptr(y2), D, B, T, H, 64, _lib.stream_handle())
+    assert torch.isfinite(y1).all() and torch.isfinite(st).all()
+    assert float((y1 - y2).abs().max()) < 1e-5 * float(y2.abs().max())
+    assert float((st - st2).abs().max()) < 1e-5 * float(st2.abs().max())
+    with pytest.raises(_lib.HipKernelError):     # workspace too small
+        _lib.call("rwkvq_wkv7_scan_chunked", _lib.ptr(dev[0]), D,
+                  _lib.ptr(dev[1]), _lib.ptr(dev[2]), _lib.ptr(dev[3]),
+                  _lib.ptr(dev[4]), _lib.ptr(dev[5]), D, _lib.ptr(st),
+                  _lib.ptr(st), _lib.ptr(y1), D, B, T, H, 64, _lib.ptr(y1),
+                  100, _lib.stream_handle())
+
+
 def test_lora_kernel_matches_matmul():
     g = torch.Generator().manual_seed(1)
     ranks = [96, 96, 64, 256]
