@@ -223,8 +223,8 @@ int rwkvq_wkv7_scan(const float* r, long r_ld, const float* w, const float* k,
  * V^T Bq, Y = S0 Ry + V^T Yq, from the cumulative log decay and a 16 x 16
  * unit triangular solve), then the chunks are applied in order on the
  * fp32 matrix cores.  ws: device workspace of at least
- * B * H * ceil(T / 16) * 6400 floats (ws_floats), 16-byte aligned; decays
- * are floored at e^-60.  Same result as the step-by-step scan to fp32
+ * B * H * NC * 6400 floats (ws_floats), NC = ceil(T / 16) rounded up to a
+ * multiple of 3, 16-byte aligned; decays are floored at e^-60.  Same result as the step-by-step scan to fp32
  * rounding (the float64 oracle bar, 1e-5 relative, holds for both).
  * Replaces: rwkv_metal.wkv7_infer for T > 1 (reference: quant_model.py:
  * 118-125, 714; math rwkv7_ref.py:236-255). */

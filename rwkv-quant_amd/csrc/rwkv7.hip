@@ -615,11 +615,16 @@ wkv_chunk_ops_k(const float* __restrict__ r, long r_ld,
   const int c = blockIdx.x % NC, bh = blockIdx.x / NC;
   const int h = bh % H, bi = bh / H;
   const int tid = threadIdx.x;
-  __shared__ float sLw[kCL][kPad], sK[kCL][kPad], sA[kCL][kPad],
-      sB[kCL][kPad], sR[kCL][kPad], sG[kCL + 1][kPad];
-  __shared__ float sM[kCL][kCL + 1], sN[kCL][kCL + 1], sBt[kCL][kCL + 1],
-      sKt[kCL][kCL + 1], sW[kCL][kCL + 1], sNW[kCL][kCL + 1];
-  __shared__ float sCW[kHead][kCL + 1], sBh[kCL][kPad], sKh[kCL][kPad];
+  // rows of 64 key channels (stride 68) and of 16 steps (stride 20), all
+  // read as float4s; matrices indexed [row][k] are stored with the summed
+  // index last (the transposes of M, N, W, Bt, Bh where that is needed)
+  constexpr int kQ = 20;
+  __shared__ __attribute__((aligned(16))) float sEw[kCL][kPad], sK[kCL][kPad],
+      sA[kCL][kPad], sB[kCL][kPad], sR[kCL][kPad], sG[kCL + 1][kPad];
+  __shared__ __attribute__((aligned(16))) float sMT[kCL][kQ], sNT[kCL][kQ],
+      sBtT[kCL][kQ], sKt[kCL][kQ], sWT[kCL][kQ], sNW[kCL][kQ];
+  __shared__ __attribute__((aligned(16))) float sCW[kHead][kQ],
+      sBhT[kHead][kQ], sKh[kCL][kPad];
 
   // 1. the chunk's inputs (identity steps past T); log decay floored at
   //    -60 so that a decay of exactly 0 stays finite
@@ -634,7 +639,9 @@ wkv_chunk_ops_k(const float* __restrict__ r, long r_ld,
       av = a[row * ld + col]; bv = b[row * ld + col];
       rv = r[row * r_ld + col];
     }
-    sLw[t][kap] = fmaxf(logf(wv), -60.f);
+    const float lw = fmaxf(logf(wv), -60.f);
+    sG[t + 1][kap] = lw;                 // summed in place below
+    sEw[t][kap] = __expf(lw);
     sK[t][kap] = kv; sA[t][kap] = av; sB[t][kap] = bv; sR[t][kap] = rv;
   }
   __syncthreads();
@@ -644,28 +651,46 @@ wkv_chunk_ops_k(const float* __restrict__ r, long r_ld,
     sG[0][tid] = 0.f;
 #pragma unroll
     for (int t = 0; t < kCL; ++t) {
-      g += sLw[t][tid];
+      g += sG[t + 1][tid];
       sG[t + 1][tid] = g;
     }
   }
   __syncthreads();
-  // 3. the L x L products (thread = (t, j)) and Bh, Kh
+  // 3. the L x L products (thread = (t, j)), four key channels per LDS
+  //    read; e^{G[t+1]-G[j+1]} = e^{G[t]-G[j+1]} w_t for j < t, 1 for j = t
   {
     const int t = tid >> 4, j = tid & 15;
     float m = 0.f, n = 0.f, bt = 0.f, kt = 0.f;
-    for (int kap = 0; kap < kHead; ++kap) {
-      const float gj = sG[j + 1][kap], bj = sB[j][kap], kj = sK[j][kap];
-      const float e1 = j < t ? __expf(sG[t][kap] - gj) * sA[t][kap] : 0.f;
-      const float e2 = j <= t ? __expf(sG[t + 1][kap] - gj) * sR[t][kap] : 0.f;
-      m += bj * e1; n += kj * e1;
-      bt += bj * e2; kt += kj * e2;
+    const float4* pGj = reinterpret_cast<const float4*>(&sG[j + 1][0]);
+    const float4* pB = reinterpret_cast<const float4*>(&sB[j][0]);
+    const float4* pK = reinterpret_cast<const float4*>(&sK[j][0]);
+    const float4* pGt = reinterpret_cast<const float4*>(&sG[t][0]);
+    const float4* pA = reinterpret_cast<const float4*>(&sA[t][0]);
+    const float4* pE = reinterpret_cast<const float4*>(&sEw[t][0]);
+    const float4* pR = reinterpret_cast<const float4*>(&sR[t][0]);
+    const bool lt = j < t, eq = j == t;
+    for (int q = 0; q < kHead / 4; ++q) {
+      const float4 gj = pGj[q], bj = pB[q], kj = pK[q], gt = pGt[q],
+                   at = pA[q], et = pE[q], rt = pR[q];
+      const float gjs[4] = {gj.x, gj.y, gj.z, gj.w}, bjs[4] = {bj.x, bj.y, bj.z, bj.w};
+      const float kjs[4] = {kj.x, kj.y, kj.z, kj.w}, gts[4] = {gt.x, gt.y, gt.z, gt.w};
+      const float ats[4] = {at.x, at.y, at.z, at.w}, ets[4] = {et.x, et.y, et.z, et.w};
+      const float rts[4] = {rt.x, rt.y, rt.z, rt.w};
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float d = lt ? __expf(gts[u] - gjs[u]) : 0.f;
+        const float e1 = d * ats[u];
+        const float e2 = (lt ? d * ets[u] : (eq ? 1.f : 0.f)) * rts[u];
+        m += bjs[u] * e1; n += kjs[u] * e1;
+        bt += bjs[u] * e2; kt += kjs[u] * e2;
+      }
     }
-    sM[t][j] = m; sN[t][j] = n; sBt[j][t] = bt; sKt[j][t] = kt;
+    sMT[j][t] = m; sNT[j][t] = n; sBtT[t][j] = bt; sKt[j][t] = kt;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int idx = tid + 256 * e, jj = idx >> 6, mu = idx & 63;
       const float d = __expf(sG[kCL][mu] - sG[jj + 1][mu]);
-      sBh[jj][mu] = sB[jj][mu] * d;
+      sBhT[mu][jj] = sB[jj][mu] * d;
       sKh[jj][mu] = sK[jj][mu] * d;
     }
   }
@@ -679,79 +704,88 @@ wkv_chunk_ops_k(const float* __restrict__ r, long r_ld,
     for (int i = kCL - 1; i >= 0; --i) {
       float sum = 0.f;
 #pragma unroll
-      for (int m2 = i + 1; m2 < kCL; ++m2) sum += sM[m2][i] * col[m2];
+      for (int m2 = i + 1; m2 < kCL; ++m2) sum += sMT[i][m2] * col[m2];
       col[i] = i == cc ? 1.f : (i > cc ? 0.f : sum);
     }
 #pragma unroll
-    for (int i = 0; i < kCL; ++i) sW[i][cc] = col[i];
+    for (int q = 0; q < kCL / 4; ++q)
+      *reinterpret_cast<float4*>(&sWT[cc][4 * q]) =
+          make_float4(col[4 * q], col[4 * q + 1], col[4 * q + 2], col[4 * q + 3]);
   }
   __syncthreads();
+  // dot of two 16-float LDS rows
+  auto dot16 = [](const float* x, const float* y) {
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    const float4* y4 = reinterpret_cast<const float4*>(y);
+    float acc = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float4 p = x4[q], v2 = y4[q];
+      acc += (p.x * v2.x + p.y * v2.y) + (p.z * v2.z + p.w * v2.w);
+    }
+    return acc;
+  };
   // 5. CW = C W (thread = key channel x 4 columns), NW = N^T W
   {
     const int kap = tid >> 2, cq = tid & 3;
-    float cv[kCL];
+    __shared__ __attribute__((aligned(16))) float sC[kHead][kQ];
 #pragma unroll
-    for (int t = 0; t < kCL; ++t) cv[t] = __expf(sG[t][kap]) * sA[t][kap];
+    for (int q = 0; q < 4; ++q) {
+      const int t = cq * 4 + q;
+      sC[kap][t] = __expf(sG[t][kap]) * sA[t][kap];
+    }
+    __syncthreads();
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int cc = cq * 4 + q;
-      float sum = 0.f;
-#pragma unroll
-      for (int t = 0; t < kCL; ++t) sum += cv[t] * sW[t][cc];
-      sCW[kap][cc] = sum;
+      sCW[kap][cc] = dot16(&sC[kap][0], &sWT[cc][0]);
     }
     const int j = tid >> 4, cc = tid & 15;
-    float sum = 0.f;
-#pragma unroll
-    for (int t = 0; t < kCL; ++t) sum += sN[t][j] * sW[t][cc];
-    sNW[j][cc] = sum;
+    sNW[j][cc] = dot16(&sNT[j][0], &sWT[cc][0]);
   }
   __syncthreads();
   // 6. the operators, written in the scan kernel's lane order
   float* o = ops + ((size_t)bh * NC + c) * kOpsFloats;
   for (int e = 0; e < 16; ++e) {
     const int idx = tid + 256 * e;
-    const int s = idx & 15, l = (idx >> 4) & 63, wv = idx >> 10;
-    const int kap = 4 * s + (l >> 4), mu = 16 * wv + (l & 15);
-    float acc = kap == mu ? __expf(sG[kCL][kap]) : 0.f;
-#pragma unroll
-    for (int j = 0; j < kCL; ++j) acc += sCW[kap][j] * sBh[j][mu];
-    o[idx] = acc;
+    const int s2 = idx & 15, l = (idx >> 4) & 63, wv = idx >> 10;
+    const int kap = 4 * s2 + (l >> 4), mu = 16 * wv + (l & 15);
+    const float diag = kap == mu ? __expf(sG[kCL][kap]) : 0.f;
+    o[idx] = diag + dot16(&sCW[kap][0], &sBhT[mu][0]);
   }
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const int idx = tid + 256 * e;
-    const int s = idx & 3, l = (idx >> 2) & 63, wv = idx >> 8;
+    const int s2 = idx & 3, l = (idx >> 2) & 63, wv = idx >> 8;
     {
-      const int j = 4 * s + (l >> 4), mu = 16 * wv + (l & 15);
-      float acc = sKh[j][mu];
-#pragma unroll
-      for (int m2 = 0; m2 < kCL; ++m2) acc += sNW[j][m2] * sBh[m2][mu];
-      o[4096 + idx] = acc;
+      const int j = 4 * s2 + (l >> 4), mu = 16 * wv + (l & 15);
+      o[4096 + idx] = sKh[j][mu] + dot16(&sNW[j][0], &sBhT[mu][0]);
     }
     {
-      const int kap = 16 * wv + 4 * s + (l >> 4), t = l & 15;
-      float acc = __expf(sG[t + 1][kap]) * sR[t][kap];
-#pragma unroll
-      for (int j = 0; j < kCL; ++j) acc += sCW[kap][j] * sBt[j][t];
-      o[5120 + idx] = acc;
+      const int kap = 16 * wv + 4 * s2 + (l >> 4), t = l & 15;
+      o[5120 + idx] = __expf(sG[t + 1][kap]) * sR[t][kap] +
+                      dot16(&sCW[kap][0], &sBtT[t][0]);
     }
   }
   {
-    const int s = tid & 3, l = tid >> 2;
-    const int j = 4 * s + (l >> 4), t = l & 15;
-    float acc = sKt[j][t];
-#pragma unroll
-    for (int m2 = 0; m2 < kCL; ++m2) acc += sNW[j][m2] * sBt[m2][t];
-    o[6144 + tid] = acc;
+    const int s2 = tid & 3, l = tid >> 2;
+    const int j = 4 * s2 + (l >> 4), t = l & 15;
+    o[6144 + tid] = sKt[j][t] + dot16(&sNW[j][0], &sBtT[t][0]);
   }
 }
 
 // The sequential part: block = 16 value rows of one (sequence, head), 4
 // waves; per chunk wave w computes columns 16w..16w+15 of S0 P + V^T Bq and
 // key steps 16w..16w+15 of S0 Ry (wave 0 adds V^T Yq); the new rows and the
-// partial outputs meet in LDS.  The next chunk's operators and values are
-// loaded before the current chunk's products.
+// partial outputs meet in LDS (double-buffered: one barrier per chunk).
+// Each chunk's operators and values are loaded three chunks ahead, into
+// three register sets used in turn (compile-time indices, no copies).
+struct ChunkOps {
+  float4 pf[4];
+  float4 bq, ry, yq;
+  float vv[4];
+};
+
 __global__ void __launch_bounds__(256)
 wkv_chunk_scan_k(const float* __restrict__ v, long ld,
                  const float* __restrict__ ops, const float* state_in,
@@ -763,8 +797,8 @@ wkv_chunk_scan_k(const float* __restrict__ v, long ld,
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int li = lane & 15, lg = lane >> 4;
-  __shared__ __attribute__((aligned(16))) float sS[4][16][16];   // [k%4][row][k/4]
-  __shared__ float sY[4][4][64];                                // [wave][v][lane]
+  __shared__ __attribute__((aligned(16))) float sS[2][4][16][16];  // [buf][k%4][row][k/4]
+  __shared__ float sY[2][4][4][64];                              // [buf][wave][q][lane]
 
   // A fragments of the rows: aS[s] = S[row0 + li][4 s + lg]
   float aS[16];
@@ -774,41 +808,44 @@ wkv_chunk_scan_k(const float* __restrict__ v, long ld,
     for (int s = 0; s < 16; ++s) aS[s] = st[4 * s + lg];
   }
   const float* opsb = ops + (size_t)bh * NC * kOpsFloats;
-  auto load_ops = [&](int c, float4 (&pf)[4], float4& bq, float4& ry,
-                      float4& yq, float (&vv)[4]) {
+  auto load_ops = [&](int c, ChunkOps& co) {
+    c = min(c, NC - 1);                      // past the end: reloads, unused
     const float* o = opsb + (size_t)c * kOpsFloats;
     const float4* p4 = reinterpret_cast<const float4*>(o + (wv * 64 + lane) * 16);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) pf[q] = p4[q];
-    bq = *reinterpret_cast<const float4*>(o + 4096 + (wv * 64 + lane) * 4);
-    ry = *reinterpret_cast<const float4*>(o + 5120 + (wv * 64 + lane) * 4);
-    yq = *reinterpret_cast<const float4*>(o + 6144 + lane * 4);
+    for (int q = 0; q < 4; ++q) co.pf[q] = p4[q];
+    co.bq = *reinterpret_cast<const float4*>(o + 4096 + (wv * 64 + lane) * 4);
+    co.ry = *reinterpret_cast<const float4*>(o + 5120 + (wv * 64 + lane) * 4);
+    co.yq = *reinterpret_cast<const float4*>(o + 6144 + lane * 4);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
+      // unconditional load of a clamped step, kept as loaded (zeroed past
+      // T where it is used): the compiler's load counting stays exact and
+      // nothing waits for the load before its chunk
       const int tg = c * kCL + 4 * s + lg;
-      vv[s] = tg < T ? v[((size_t)bi * T + tg) * ld + (size_t)h * kHead + row0 + li]
-                     : 0.f;
+      co.vv[s] =
+          v[((size_t)bi * T + min(tg, T - 1)) * ld + (size_t)h * kHead + row0 + li];
     }
   };
-  float4 pf[4], bq, ry, yq, pf2[4], bq2, ry2, yq2;
-  float vv[4], vv2[4];
-  load_ops(0, pf, bq, ry, yq, vv);
-  for (int c = 0; c < NC; ++c) {
-    const int cn = min(c + 1, NC - 1);
-    load_ops(cn, pf2, bq2, ry2, yq2, vv2);
-    const float pfs[16] = {pf[0].x, pf[0].y, pf[0].z, pf[0].w, pf[1].x, pf[1].y,
-                           pf[1].z, pf[1].w, pf[2].x, pf[2].y, pf[2].z, pf[2].w,
-                           pf[3].x, pf[3].y, pf[3].z, pf[3].w};
-    const float bqs[4] = {bq.x, bq.y, bq.z, bq.w};
-    const float rys[4] = {ry.x, ry.y, ry.z, ry.w};
-    const float yqs[4] = {yq.x, yq.y, yq.z, yq.w};
+  auto chunk = [&](int c, const ChunkOps& co) {
+    const int p = c & 1;
+    const float pfs[16] = {co.pf[0].x, co.pf[0].y, co.pf[0].z, co.pf[0].w,
+                           co.pf[1].x, co.pf[1].y, co.pf[1].z, co.pf[1].w,
+                           co.pf[2].x, co.pf[2].y, co.pf[2].z, co.pf[2].w,
+                           co.pf[3].x, co.pf[3].y, co.pf[3].z, co.pf[3].w};
+    const float bqs[4] = {co.bq.x, co.bq.y, co.bq.z, co.bq.w};
+    const float rys[4] = {co.ry.x, co.ry.y, co.ry.z, co.ry.w};
+    const float yqs[4] = {co.yq.x, co.yq.y, co.yq.z, co.yq.w};
+    float vvs[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) vvs[s] = c * kCL + 4 * s + lg < T ? co.vv[s] : 0.f;
     f32x4c_t accS = {0.f, 0.f, 0.f, 0.f}, accY = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < 16; ++s)
       accS = __builtin_amdgcn_mfma_f32_16x16x4f32(aS[s], pfs[s], accS, 0, 0, 0);
 #pragma unroll
     for (int s = 0; s < 4; ++s)
-      accS = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[s], bqs[s], accS, 0, 0, 0);
+      accS = __builtin_amdgcn_mfma_f32_16x16x4f32(vvs[s], bqs[s], accS, 0, 0, 0);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const float av = wv == 0 ? aS[s] : wv == 1 ? aS[4 + s]
@@ -818,47 +855,53 @@ wkv_chunk_scan_k(const float* __restrict__ v, long ld,
     if (wv == 0) {
 #pragma unroll
       for (int s = 0; s < 4; ++s)
-        accY = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[s], yqs[s], accY, 0, 0, 0);
+        accY = __builtin_amdgcn_mfma_f32_16x16x4f32(vvs[s], yqs[s], accY, 0, 0, 0);
     }
     // lane holds new S[4 lg + q][16 wv + li] and partial Y[4 lg + q][li]
-    {
-      const int kcol = 16 * wv + li;
+    const int kcol = 16 * wv + li;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        sS[kcol & 3][4 * lg + q][kcol >> 2] = accS[q];
-        sY[wv][q][lane] = accY[q];
-      }
+    for (int q = 0; q < 4; ++q) {
+      sS[p][kcol & 3][4 * lg + q][kcol >> 2] = accS[q];
+      sY[p][wv][q][lane] = accY[q];
     }
     __syncthreads();
-    {
-      const float4* a4 = reinterpret_cast<const float4*>(&sS[lg][li][0]);
+    const float4* a4 = reinterpret_cast<const float4*>(&sS[p][lg][li][0]);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const float4 f = a4[q];
-        aS[4 * q] = f.x; aS[4 * q + 1] = f.y; aS[4 * q + 2] = f.z; aS[4 * q + 3] = f.w;
-      }
-      // output element (row i, step t) of this chunk: C layout lane
-      // t + 16 (i / 4), register i % 4
-      const int i = threadIdx.x & 15, t = threadIdx.x >> 4;
-      const int tg = c * kCL + t;
-      const int src = t + 16 * (i >> 2), q = i & 3;
-      const float yv = (sY[0][q][src] + sY[1][q][src]) + (sY[2][q][src] + sY[3][q][src]);
-      if (tg < T)
-        y[((size_t)bi * T + tg) * y_ld + (size_t)h * kHead + row0 + i] = yv;
+    for (int q = 0; q < 4; ++q) {
+      const float4 f = a4[q];
+      aS[4 * q] = f.x; aS[4 * q + 1] = f.y; aS[4 * q + 2] = f.z; aS[4 * q + 3] = f.w;
     }
-    __syncthreads();
-#pragma unroll
-    for (int q = 0; q < 4; ++q) pf[q] = pf2[q];
-    bq = bq2; ry = ry2; yq = yq2;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) vv[s] = vv2[s];
+    // output element (row i, step t) of this chunk: C layout lane
+    // t + 16 (i / 4), register i % 4
+    const int i = threadIdx.x & 15, t = threadIdx.x >> 4;
+    const int tg = c * kCL + t;
+    const int src = t + 16 * (i >> 2), q = i & 3;
+    const float yv = (sY[p][0][q][src] + sY[p][1][q][src]) +
+                     (sY[p][2][q][src] + sY[p][3][q][src]);
+    if (tg < T)
+      y[((size_t)bi * T + tg) * y_ld + (size_t)h * kHead + row0 + i] = yv;
+  };
+  // NC is a multiple of 3 (identity chunks pad the sequence), so the
+  // loop body has no branches and each wait covers only its own set
+  ChunkOps o0, o1, o2;
+  load_ops(0, o0);
+  load_ops(1, o1);
+  load_ops(2, o2);
+  for (int c = 0; c < NC; c += 3) {
+    chunk(c, o0);
+    load_ops(c + 3, o0);
+    chunk(c + 1, o1);
+    load_ops(c + 4, o1);
+    chunk(c + 2, o2);
+    load_ops(c + 5, o2);
   }
-  // final rows (aS holds them in A-fragment order; sS in [k%4][row][k/4])
+  // final rows, from the last chunk's buffer ([k%4][row][k/4])
+  const int pl = (NC - 1) & 1;
   float* so = state_out + ((size_t)bh * kHead + row0) * kHead;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const int idx = threadIdx.x + 256 * e, rr = idx >> 6, kk = idx & 63;
-    so[(size_t)rr * kHead + kk] = sS[kk & 3][rr][kk >> 2];
+    so[(size_t)rr * kHead + kk] = sS[pl][kk & 3][rr][kk >> 2];
   }
 }
 
@@ -935,7 +978,9 @@ int rwkvq_wkv7_scan_chunked(const float* r, long r_ld, const float* w,
   if (B <= 0 || T <= 0 || H <= 0 || head_size != kHead || ld < H * kHead ||
       r_ld < H * kHead || y_ld < H * kHead || !ws || !state_out)
     return RWKVQ_ERR_ARG;
-  const int NC = (T + kCL - 1) / kCL;
+  // chunks padded to a multiple of 3 with identity steps (the sequential
+  // kernel walks them three at a time)
+  const int NC = ((T + kCL - 1) / kCL + 2) / 3 * 3;
   if (ws_floats < (long)B * H * NC * kOpsFloats || ((uintptr_t)ws & 15))
     return RWKVQ_ERR_ARG;
   hipLaunchKernelGGL(wkv_chunk_ops_k, dim3(B * H * NC), dim3(256), 0,

@@ -532,7 +532,7 @@ class QuantRWKV7:
                   _lib.ptr(wk.w), _lib.ptr(wk.kp), _lib.ptr(wk.vp),
                   _lib.ptr(wk.aa), _lib.ptr(wk.bb), N, C, self.head_size, st)
         if T >= WKV_CHUNK_MIN_T:
-            need = B * H * (-(-T // 16)) * WKV_CHUNK_OPS
+            need = B * H * (-(-(-(-T // 16)) // 3) * 3) * WKV_CHUNK_OPS
             ops = getattr(wk, "wkv_ops", None)
             if ops is None or ops.numel() < need:
                 # allocated by the warm-up run that precedes any capture

@@ -90,7 +90,8 @@ def test_shift_lerp_matches_float64(B, T, nc, prev):
 
 def _scan_chunked(dev, st_in, st_out, y, B, T, H):
     D = H * 64
-    ws = torch.empty(B * H * (-(-T // 16)) * 6400, device="cuda")
+    nc = -(-(-(-T // 16)) // 3) * 3           # chunks, padded to 3k
+    ws = torch.empty(B * H * nc * 6400, device="cuda")
     _lib.call("rwkvq_wkv7_scan_chunked", _lib.ptr(dev[0]), D,
               _lib.ptr(dev[1]), _lib.ptr(dev[2]), _lib.ptr(dev[3]),
               _lib.ptr(dev[4]), _lib.ptr(dev[5]), D, _lib.ptr(st_in),
