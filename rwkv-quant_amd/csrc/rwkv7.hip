@@ -601,12 +601,21 @@ constexpr int kPad = 68;                // LDS row stride (floats)
 
 typedef float f32x4c_t __attribute__((ext_vector_type(4)));
 
-// Operator block of one chunk, in the lane order the scan kernel's fp32
-// MFMA (16x16x4: lane l holds A[l%16][l/16], B[l/16][l%16]) reads:
-//   [0, 4096)     Pf [w][l][s]  = P[4s + l/16][16w + l%16]      s < 16
-//   [4096, 5120)  Bqf[w][l][s]  = Bq[4s + l/16][16w + l%16]     s < 4
-//   [5120, 6144)  Ryf[w][l][s]  = Ry[16w + 4s + l/16][l%16]     s < 4
-//   [6144, 6400)  Yqf[l][s]     = Yq[4s + l/16][l%16]           s < 4
+// One 16x16x4 fp32 matrix-core step: D = A B + C, lane l holding A[l%16][l/16],
+// B[l/16][l%16] and D[4 (l/16) + v][l%16].
+__device__ __forceinline__ f32x4c_t mfma4(float a, float b, f32x4c_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Operator block of one chunk, in the register order the scan kernel's
+// fp32 MFMAs use.  Lane l = 16 g + m of wave w; the scan's key steps run
+// in the order k(s, g) = 16 (s / 4) + 4 g + s % 4, its value steps in the
+// order j(s, g) = 4 g + s:
+//   [0, 4096)     Pf [w][l][s] = P[k(s, g)][16 w + m]           s < 16
+//   [4096, 5120)  Bqf[w][l][s] = Bq[4 g + s][16 w + m]          s < 4
+//   [5120, 6144)  Ryf[w][l][s] = Ry[16 w + 4 g + s][m]          s < 4
+//   [6144, 6400)  Yqf[l][s]    = Yq[4 g + s][m]                 s < 4
+// -- exactly the accumulator registers of the MFMAs that produce them.
 __global__ void __launch_bounds__(256)
 wkv_chunk_ops_k(const float* __restrict__ r, long r_ld,
                 const float* __restrict__ w, const float* __restrict__ k,
@@ -615,16 +624,16 @@ wkv_chunk_ops_k(const float* __restrict__ r, long r_ld,
   const int c = blockIdx.x % NC, bh = blockIdx.x / NC;
   const int h = bh % H, bi = bh / H;
   const int tid = threadIdx.x;
-  // rows of 64 key channels (stride 68) and of 16 steps (stride 20), all
-  // read as float4s; matrices indexed [row][k] are stored with the summed
-  // index last (the transposes of M, N, W, Bt, Bh where that is needed)
+  const int lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int li = lane & 15, lg = lane >> 4;
   constexpr int kQ = 20;
-  __shared__ __attribute__((aligned(16))) float sEw[kCL][kPad], sK[kCL][kPad],
-      sA[kCL][kPad], sB[kCL][kPad], sR[kCL][kPad], sG[kCL + 1][kPad];
-  __shared__ __attribute__((aligned(16))) float sMT[kCL][kQ], sNT[kCL][kQ],
-      sBtT[kCL][kQ], sKt[kCL][kQ], sWT[kCL][kQ], sNW[kCL][kQ];
-  __shared__ __attribute__((aligned(16))) float sCW[kHead][kQ],
-      sBhT[kHead][kQ], sKh[kCL][kPad];
+  // [step][key channel] rows (stride 68); 16 x 16 matrices (stride 20)
+  __shared__ float sEw[kCL][kPad], sK[kCL][kPad], sA[kCL][kPad],
+      sB[kCL][kPad], sR[kCL][kPad], sG[kCL + 1][kPad];
+  __shared__ float sYa[kCL][kPad], sYr[kCL][kPad], sXb[kCL][kPad],
+      sXk[kCL][kPad], sBh[kCL][kPad], sKh[kCL][kPad];
+  __shared__ float sM[kCL][kQ], sN[kCL][kQ], sBt[kCL][kQ], sKt[kCL][kQ],
+      sW[kCL][kQ], sNW[kCL][kQ], sCW[kHead][kQ];
 
   // 1. the chunk's inputs (identity steps past T); log decay floored at
   //    -60 so that a decay of exactly 0 stays finite
@@ -632,20 +641,22 @@ wkv_chunk_ops_k(const float* __restrict__ r, long r_ld,
   for (int e = 0; e < 4; ++e) {
     const int idx = tid + 256 * e, t = idx >> 6, kap = idx & 63;
     const int tg = c * kCL + t;
-    float wv = 1.f, kv = 0.f, av = 0.f, bv = 0.f, rv = 0.f;
+    float wvl = 1.f, kv = 0.f, av = 0.f, bv = 0.f, rv = 0.f;
     if (tg < T) {
       const size_t row = (size_t)bi * T + tg, col = (size_t)h * kHead + kap;
-      wv = w[row * ld + col]; kv = k[row * ld + col];
+      wvl = w[row * ld + col]; kv = k[row * ld + col];
       av = a[row * ld + col]; bv = b[row * ld + col];
       rv = r[row * r_ld + col];
     }
-    const float lw = fmaxf(logf(wv), -60.f);
+    const float lw = fmaxf(logf(wvl), -60.f);
     sG[t + 1][kap] = lw;                 // summed in place below
     sEw[t][kap] = __expf(lw);
     sK[t][kap] = kv; sA[t][kap] = av; sB[t][kap] = bv; sR[t][kap] = rv;
   }
   __syncthreads();
-  // 2. cumulative log decay per key channel
+  // 2. cumulative log decay per key channel; the factored products below
+  //    need e^{-G} finite (G[16] >= -80 on every channel)
+  bool ok = true;
   if (tid < kHead) {
     float g = 0.f;
     sG[0][tid] = 0.f;
@@ -654,48 +665,58 @@ wkv_chunk_ops_k(const float* __restrict__ r, long r_ld,
       g += sG[t + 1][tid];
       sG[t + 1][tid] = g;
     }
+    ok = g >= -80.f;
+  }
+  const bool factored = __syncthreads_and(ok);
+  // 3. decayed rows: Ya[t] = a_t e^{G[t]}, Yr[t] = r_t e^{G[t+1]} (<= 1),
+  //    Xb[j] = b_j e^{-G[j+1]}, Xk[j] = k_j e^{-G[j+1]}, Bh, Kh
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int idx = tid + 256 * e, t = idx >> 6, kap = idx & 63;
+    const float g0 = sG[t][kap], g1 = sG[t + 1][kap], gl = sG[kCL][kap];
+    sYa[t][kap] = sA[t][kap] * __expf(g0);
+    sYr[t][kap] = sR[t][kap] * __expf(g1);
+    const float inv = factored ? __expf(-g1) : 0.f;
+    sXb[t][kap] = sB[t][kap] * inv;
+    sXk[t][kap] = sK[t][kap] * inv;
+    const float d = __expf(gl - g1);
+    sBh[t][kap] = sB[t][kap] * d;
+    sKh[t][kap] = sK[t][kap] * d;
   }
   __syncthreads();
-  // 3. the L x L products (thread = (t, j)), four key channels per LDS
-  //    read; e^{G[t+1]-G[j+1]} = e^{G[t]-G[j+1]} w_t for j < t, 1 for j = t
-  {
+  // 4. M[t][j] = Ya[t].Xb[j] (j < t), N[t][j] = Ya[t].Xk[j] (j < t),
+  //    Bt[j][t] = Xb[j].Yr[t], Kt[j][t] = Xk[j].Yr[t] (j <= t): one 16 x 16
+  //    x 64 product per wave; exact pairwise decays when e^{-G} would not
+  //    be finite
+  if (factored) {
+    const float(*pA)[kPad] = wv < 2 ? sYa : wv == 2 ? sXb : sXk;
+    const float(*pB)[kPad] = wv == 0 ? sXb : wv == 1 ? sXk : sYr;
+    f32x4c_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s2 = 0; s2 < 16; ++s2)
+      acc = mfma4(pA[li][4 * s2 + lg], pB[li][4 * s2 + lg], acc);
+    float(*dst)[kQ] = wv == 0 ? sM : wv == 1 ? sN : wv == 2 ? sBt : sKt;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int row = 4 * lg + q, col = li;   // (t, j) for M, N; (j, t) else
+      const bool keep = wv < 2 ? col < row : row <= col;
+      dst[row][col] = keep ? acc[q] : 0.f;
+    }
+  } else {
     const int t = tid >> 4, j = tid & 15;
     float m = 0.f, n = 0.f, bt = 0.f, kt = 0.f;
-    const float4* pGj = reinterpret_cast<const float4*>(&sG[j + 1][0]);
-    const float4* pB = reinterpret_cast<const float4*>(&sB[j][0]);
-    const float4* pK = reinterpret_cast<const float4*>(&sK[j][0]);
-    const float4* pGt = reinterpret_cast<const float4*>(&sG[t][0]);
-    const float4* pA = reinterpret_cast<const float4*>(&sA[t][0]);
-    const float4* pE = reinterpret_cast<const float4*>(&sEw[t][0]);
-    const float4* pR = reinterpret_cast<const float4*>(&sR[t][0]);
     const bool lt = j < t, eq = j == t;
-    for (int q = 0; q < kHead / 4; ++q) {
-      const float4 gj = pGj[q], bj = pB[q], kj = pK[q], gt = pGt[q],
-                   at = pA[q], et = pE[q], rt = pR[q];
-      const float gjs[4] = {gj.x, gj.y, gj.z, gj.w}, bjs[4] = {bj.x, bj.y, bj.z, bj.w};
-      const float kjs[4] = {kj.x, kj.y, kj.z, kj.w}, gts[4] = {gt.x, gt.y, gt.z, gt.w};
-      const float ats[4] = {at.x, at.y, at.z, at.w}, ets[4] = {et.x, et.y, et.z, et.w};
-      const float rts[4] = {rt.x, rt.y, rt.z, rt.w};
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const float d = lt ? __expf(gts[u] - gjs[u]) : 0.f;
-        const float e1 = d * ats[u];
-        const float e2 = (lt ? d * ets[u] : (eq ? 1.f : 0.f)) * rts[u];
-        m += bjs[u] * e1; n += kjs[u] * e1;
-        bt += bjs[u] * e2; kt += kjs[u] * e2;
-      }
+    for (int kap = 0; kap < kHead; ++kap) {
+      const float d = lt ? __expf(sG[t][kap] - sG[j + 1][kap]) : 0.f;
+      const float e1 = d * sA[t][kap];
+      const float e2 = (lt ? d * sEw[t][kap] : (eq ? 1.f : 0.f)) * sR[t][kap];
+      m += sB[j][kap] * e1; n += sK[j][kap] * e1;
+      bt += sB[j][kap] * e2; kt += sK[j][kap] * e2;
     }
-    sMT[j][t] = m; sNT[j][t] = n; sBtT[t][j] = bt; sKt[j][t] = kt;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int idx = tid + 256 * e, jj = idx >> 6, mu = idx & 63;
-      const float d = __expf(sG[kCL][mu] - sG[jj + 1][mu]);
-      sBhT[mu][jj] = sB[jj][mu] * d;
-      sKh[jj][mu] = sK[jj][mu] * d;
-    }
+    sM[t][j] = m; sN[t][j] = n; sBt[j][t] = bt; sKt[j][t] = kt;
   }
   __syncthreads();
-  // 4. W = (I - M^T)^-1 (unit upper triangular), one column per thread:
+  // 5. W = (I - M^T)^-1 (unit upper triangular), one column per lane:
   //    W[i][cc] = sum_{m > i} M[m][i] W[m][cc], W[cc][cc] = 1
   if (tid < kCL) {
     const int cc = tid;
@@ -704,80 +725,87 @@ wkv_chunk_ops_k(const float* __restrict__ r, long r_ld,
     for (int i = kCL - 1; i >= 0; --i) {
       float sum = 0.f;
 #pragma unroll
-      for (int m2 = i + 1; m2 < kCL; ++m2) sum += sMT[i][m2] * col[m2];
+      for (int m2 = i + 1; m2 < kCL; ++m2) sum += sM[m2][i] * col[m2];
       col[i] = i == cc ? 1.f : (i > cc ? 0.f : sum);
     }
 #pragma unroll
-    for (int q = 0; q < kCL / 4; ++q)
-      *reinterpret_cast<float4*>(&sWT[cc][4 * q]) =
-          make_float4(col[4 * q], col[4 * q + 1], col[4 * q + 2], col[4 * q + 3]);
+    for (int i = 0; i < kCL; ++i) sW[i][cc] = col[i];
   }
   __syncthreads();
-  // dot of two 16-float LDS rows
-  auto dot16 = [](const float* x, const float* y) {
-    const float4* x4 = reinterpret_cast<const float4*>(x);
-    const float4* y4 = reinterpret_cast<const float4*>(y);
-    float acc = 0.f;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const float4 p = x4[q], v2 = y4[q];
-      acc += (p.x * v2.x + p.y * v2.y) + (p.z * v2.z + p.w * v2.w);
-    }
-    return acc;
-  };
-  // 5. CW = C W (thread = key channel x 4 columns), NW = N^T W
+  // 6. CW = Ya^T W (wave w: key channels 16w..16w+15), NW = N^T W (wave 0)
   {
-    const int kap = tid >> 2, cq = tid & 3;
-    __shared__ __attribute__((aligned(16))) float sC[kHead][kQ];
+    f32x4c_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int t = cq * 4 + q;
-      sC[kap][t] = __expf(sG[t][kap]) * sA[t][kap];
-    }
-    __syncthreads();
+    for (int s2 = 0; s2 < 4; ++s2)
+      acc = mfma4(sYa[4 * s2 + lg][16 * wv + li], sW[4 * s2 + lg][li], acc);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int cc = cq * 4 + q;
-      sCW[kap][cc] = dot16(&sC[kap][0], &sWT[cc][0]);
+    for (int q = 0; q < 4; ++q) sCW[16 * wv + 4 * lg + q][li] = acc[q];
+    if (wv == 1) {
+      f32x4c_t an = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s2 = 0; s2 < 4; ++s2)
+        an = mfma4(sN[4 * s2 + lg][li], sW[4 * s2 + lg][li], an);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) sNW[4 * lg + q][li] = an[q];
     }
-    const int j = tid >> 4, cc = tid & 15;
-    sNW[j][cc] = dot16(&sNT[j][0], &sWT[cc][0]);
   }
   __syncthreads();
-  // 6. the operators, written in the scan kernel's lane order
+  // 7. the operators, accumulated straight into the scan kernel's order
   float* o = ops + ((size_t)bh * NC + c) * kOpsFloats;
-  for (int e = 0; e < 16; ++e) {
-    const int idx = tid + 256 * e;
-    const int s2 = idx & 15, l = (idx >> 4) & 63, wv = idx >> 10;
-    const int kap = 4 * s2 + (l >> 4), mu = 16 * wv + (l & 15);
-    const float diag = kap == mu ? __expf(sG[kCL][kap]) : 0.f;
-    o[idx] = diag + dot16(&sCW[kap][0], &sBhT[mu][0]);
-  }
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int idx = tid + 256 * e;
-    const int s2 = idx & 3, l = (idx >> 2) & 63, wv = idx >> 8;
-    {
-      const int j = 4 * s2 + (l >> 4), mu = 16 * wv + (l & 15);
-      o[4096 + idx] = sKh[j][mu] + dot16(&sNW[j][0], &sBhT[mu][0]);
-    }
-    {
-      const int kap = 16 * wv + 4 * s2 + (l >> 4), t = l & 15;
-      o[5120 + idx] = __expf(sG[t + 1][kap]) * sR[t][kap] +
-                      dot16(&sCW[kap][0], &sBtT[t][0]);
-    }
-  }
   {
-    const int s2 = tid & 3, l = tid >> 2;
-    const int j = 4 * s2 + (l >> 4), t = l & 15;
-    o[6144 + tid] = sKt[j][t] + dot16(&sNW[j][0], &sBtT[t][0]);
+    const int mu = 16 * wv + li;
+    float pv[16];
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti) {
+      f32x4c_t acc;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int kap = 16 * ti + 4 * lg + q;
+        acc[q] = kap == mu ? __expf(sG[kCL][kap]) : 0.f;
+      }
+#pragma unroll
+      for (int s2 = 0; s2 < 4; ++s2)
+        acc = mfma4(sCW[16 * ti + li][4 * s2 + lg], sBh[4 * s2 + lg][mu], acc);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) pv[4 * ti + q] = acc[q];
+    }
+    float4* p4 = reinterpret_cast<float4*>(o + (wv * 64 + lane) * 16);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      p4[q] = make_float4(pv[4 * q], pv[4 * q + 1], pv[4 * q + 2], pv[4 * q + 3]);
+    // Bq = Kh + NW Bh (columns 16w..), Ry = Yr^T + CW Bt (rows 16w..)
+    f32x4c_t aq, ar;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      aq[q] = sKh[4 * lg + q][mu];
+      ar[q] = sYr[li][16 * wv + 4 * lg + q];
+    }
+#pragma unroll
+    for (int s2 = 0; s2 < 4; ++s2) {
+      aq = mfma4(sNW[li][4 * s2 + lg], sBh[4 * s2 + lg][mu], aq);
+      ar = mfma4(sCW[16 * wv + li][4 * s2 + lg], sBt[4 * s2 + lg][li], ar);
+    }
+    *reinterpret_cast<float4*>(o + 4096 + (wv * 64 + lane) * 4) =
+        make_float4(aq[0], aq[1], aq[2], aq[3]);
+    *reinterpret_cast<float4*>(o + 5120 + (wv * 64 + lane) * 4) =
+        make_float4(ar[0], ar[1], ar[2], ar[3]);
+    if (wv == 0) {     // Yq = Kt + NW Bt
+      f32x4c_t ay;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) ay[q] = sKt[4 * lg + q][li];
+#pragma unroll
+      for (int s2 = 0; s2 < 4; ++s2)
+        ay = mfma4(sNW[li][4 * s2 + lg], sBt[4 * s2 + lg][li], ay);
+      *reinterpret_cast<float4*>(o + 6144 + lane * 4) =
+          make_float4(ay[0], ay[1], ay[2], ay[3]);
+    }
   }
 }
 
 // The sequential part: block = 16 value rows of one (sequence, head), 4
 // waves; per chunk wave w computes columns 16w..16w+15 of S0 P + V^T Bq and
-// key steps 16w..16w+15 of S0 Ry (wave 0 adds V^T Yq); the new rows and the
-// partial outputs meet in LDS (double-buffered: one barrier per chunk).
+// key channels 16w..16w+15 of S0 Ry (wave 0 adds V^T Yq); the new rows and
+// the partial outputs meet in LDS (double-buffered: one barrier per chunk).
 // Each chunk's operators and values are loaded three chunks ahead, into
 // three register sets used in turn (compile-time indices, no copies).
 struct ChunkOps {
@@ -797,15 +825,19 @@ wkv_chunk_scan_k(const float* __restrict__ v, long ld,
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int li = lane & 15, lg = lane >> 4;
-  __shared__ __attribute__((aligned(16))) float sS[2][4][16][16];  // [buf][k%4][row][k/4]
+  __shared__ __attribute__((aligned(16))) float sS[2][16][kPad];   // [buf][row][key]
   __shared__ float sY[2][4][4][64];                              // [buf][wave][q][lane]
 
-  // A fragments of the rows: aS[s] = S[row0 + li][4 s + lg]
+  // A fragments of the rows in the operators' key order:
+  // aS[4 ti + q] = S[row0 + li][16 ti + 4 lg + q]
   float aS[16];
   {
     const float* st = state_in + ((size_t)bh * kHead + row0 + li) * kHead;
 #pragma unroll
-    for (int s = 0; s < 16; ++s) aS[s] = st[4 * s + lg];
+    for (int ti = 0; ti < 4; ++ti) {
+      const float4 f = *reinterpret_cast<const float4*>(st + 16 * ti + 4 * lg);
+      aS[4 * ti] = f.x; aS[4 * ti + 1] = f.y; aS[4 * ti + 2] = f.z; aS[4 * ti + 3] = f.w;
+    }
   }
   const float* opsb = ops + (size_t)bh * NC * kOpsFloats;
   auto load_ops = [&](int c, ChunkOps& co) {
@@ -822,7 +854,7 @@ wkv_chunk_scan_k(const float* __restrict__ v, long ld,
       // unconditional load of a clamped step, kept as loaded (zeroed past
       // T where it is used): the compiler's load counting stays exact and
       // nothing waits for the load before its chunk
-      const int tg = c * kCL + 4 * s + lg;
+      const int tg = c * kCL + 4 * lg + s;
       co.vv[s] =
           v[((size_t)bi * T + min(tg, T - 1)) * ld + (size_t)h * kHead + row0 + li];
     }
@@ -838,38 +870,41 @@ wkv_chunk_scan_k(const float* __restrict__ v, long ld,
     const float yqs[4] = {co.yq.x, co.yq.y, co.yq.z, co.yq.w};
     float vvs[4];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) vvs[s] = c * kCL + 4 * s + lg < T ? co.vv[s] : 0.f;
-    f32x4c_t accS = {0.f, 0.f, 0.f, 0.f}, accY = {0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < 4; ++s) vvs[s] = c * kCL + 4 * lg + s < T ? co.vv[s] : 0.f;
+    // two accumulators halve the dependent chain
+    f32x4c_t accS = {0.f, 0.f, 0.f, 0.f}, accS2 = {0.f, 0.f, 0.f, 0.f};
+    f32x4c_t accY = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < 16; ++s)
-      accS = __builtin_amdgcn_mfma_f32_16x16x4f32(aS[s], pfs[s], accS, 0, 0, 0);
+    for (int s = 0; s < 16; s += 2) {
+      accS = mfma4(aS[s], pfs[s], accS);
+      accS2 = mfma4(aS[s + 1], pfs[s + 1], accS2);
+    }
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
-      accS = __builtin_amdgcn_mfma_f32_16x16x4f32(vvs[s], bqs[s], accS, 0, 0, 0);
+    for (int s = 0; s < 4; s += 2) {
+      accS = mfma4(vvs[s], bqs[s], accS);
+      accS2 = mfma4(vvs[s + 1], bqs[s + 1], accS2);
+    }
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const float av = wv == 0 ? aS[s] : wv == 1 ? aS[4 + s]
                      : wv == 2 ? aS[8 + s] : aS[12 + s];
-      accY = __builtin_amdgcn_mfma_f32_16x16x4f32(av, rys[s], accY, 0, 0, 0);
+      accY = mfma4(av, rys[s], accY);
     }
     if (wv == 0) {
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
-        accY = __builtin_amdgcn_mfma_f32_16x16x4f32(vvs[s], yqs[s], accY, 0, 0, 0);
+      for (int s = 0; s < 4; ++s) accY = mfma4(vvs[s], yqs[s], accY);
     }
     // lane holds new S[4 lg + q][16 wv + li] and partial Y[4 lg + q][li]
-    const int kcol = 16 * wv + li;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      sS[p][kcol & 3][4 * lg + q][kcol >> 2] = accS[q];
+      sS[p][4 * lg + q][16 * wv + li] = accS[q] + accS2[q];
       sY[p][wv][q][lane] = accY[q];
     }
     __syncthreads();
-    const float4* a4 = reinterpret_cast<const float4*>(&sS[p][lg][li][0]);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const float4 f = a4[q];
-      aS[4 * q] = f.x; aS[4 * q + 1] = f.y; aS[4 * q + 2] = f.z; aS[4 * q + 3] = f.w;
+    for (int ti = 0; ti < 4; ++ti) {
+      const float4 f = *reinterpret_cast<const float4*>(&sS[p][li][16 * ti + 4 * lg]);
+      aS[4 * ti] = f.x; aS[4 * ti + 1] = f.y; aS[4 * ti + 2] = f.z; aS[4 * ti + 3] = f.w;
     }
     // output element (row i, step t) of this chunk: C layout lane
     // t + 16 (i / 4), register i % 4
@@ -895,13 +930,13 @@ wkv_chunk_scan_k(const float* __restrict__ v, long ld,
     chunk(c + 2, o2);
     load_ops(c + 5, o2);
   }
-  // final rows, from the last chunk's buffer ([k%4][row][k/4])
+  // final rows, from the last chunk's buffer
   const int pl = (NC - 1) & 1;
   float* so = state_out + ((size_t)bh * kHead + row0) * kHead;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const int idx = threadIdx.x + 256 * e, rr = idx >> 6, kk = idx & 63;
-    so[(size_t)rr * kHead + kk] = sS[pl][kk & 3][rr][kk >> 2];
+    so[(size_t)rr * kHead + kk] = sS[pl][rr][kk];
   }
 }
 
