@@ -276,6 +276,17 @@ int rwkvq_wkv7_decode_lora(const float* rkv, const float* const* h,
                            float* out, int B, int H, int head_size,
                            void* stream);
 
+/* rwkvq_gemm_f16 over up to 8 segments of unequal height (seg_rows[j] a
+ * multiple of 128) of one matrix w [sum rows, in]: segment j reads
+ * x[t * x_ld + j * in + c] and writes columns [sum_{i<j} rows_i, ...) of
+ * y [M, sum rows] with epilogue field j of seg_modes.  in % 128 == 0.
+ * Replaces: the down products of QuantTMix._lora in prefill, all
+ * branches in one launch, each padded only to 128 rows (reference:
+ * quant_model.py:462-526). */
+int rwkvq_gemm_f16_seg(const uint16_t* w, int nseg, const int* seg_rows,
+                       int in, const float* x, long x_ld, float* y, int M,
+                       int seg_modes, void* stream);
+
 /* Dense fp16 rows in up to 8 segments of one matrix w [sum rows, in], for
  * 1..16 input rows, on the matrix cores: segment j (rows seg_rows[j], a
  * multiple of 16) reads x[n * x_ld + j * in + c] and writes

@@ -56,6 +56,10 @@ struct GemmArgs {
   int M, N, in, out_per, mode;
   int seg_modes;         // mode RWKVQ_EPI_PER_SEG: 4 bits per segment
   int nt, mt;            // tile counts along N and M
+  // segment table (rwkvq_gemm_f16_seg): segment j holds rows
+  // [seg_end[j-1], seg_end[j]) and reads x at x + j * in; 0 = uniform
+  int nseg_tab;
+  int seg_end[8];
 };
 
 constexpr int kStepK = 128;                 // columns per K step
@@ -186,7 +190,13 @@ gemm_kernel(GemmArgs a) {
   }
   const int n0 = nt * BN;
   const int m0 = mt * BM;
-  const int seg = n0 / a.out_per;
+  int seg = n0 / a.out_per;
+  if (a.nseg_tab > 0) {                    // constant-index reads only
+    seg = 0;
+#pragma unroll
+    for (int j = 0; j < 7; ++j)
+      seg += (j + 1 < a.nseg_tab && n0 >= a.seg_end[j]) ? 1 : 0;
+  }
   const int ng = a.in >> 5, nsb = a.in >> 8;
   const int nsteps = a.in / kStepK;
   const float* xb = a.x + (size_t)seg * a.in;
@@ -392,7 +402,8 @@ int launch_gemm(const GemmArgs& a, hipStream_t s) {
   auto wgs = [&](int bn, int bm) {
     return (long)(a.N / bn) * ((a.M + bm - 1) / bm);
   };
-  const bool wide = a.out_per % 256 == 0;
+  // (segment tables: 128-row tiles, segments are multiples of 128 rows)
+  const bool wide = a.out_per % 256 == 0 && a.nseg_tab == 0;
   if (wide && wgs(256, 128) >= 256) return launch_tile<FMT, 2, 4>(a, s);
   if (wide && wgs(256, 64) >= 256) return launch_tile<FMT, 2, 2>(a, s);
   if (wgs(128, 64) >= 256) return launch_tile<FMT, 1, 2>(a, s);
@@ -474,6 +485,31 @@ int rwkvq_gemm_f16(const uint16_t* w, int rows, int in, int out_per,
     a.mode = mode;
     a.seg_modes = seg_modes;
   }
+  a.q = reinterpret_cast<const uint8_t*>(w);
+  return launch_gemm<F_F16>(a, (hipStream_t)stream);
+}
+
+int rwkvq_gemm_f16_seg(const uint16_t* w, int nseg, const int* seg_rows,
+                       int in, const float* x, long x_ld, float* y, int M,
+                       int seg_modes, void* stream) {
+  if (!w || !x || !y || nseg < 1 || nseg > 8 || in <= 0 || in % kStepK ||
+      M <= 0)
+    return RWKVQ_ERR_ARG;
+  int rows = 0;
+  GemmArgs a{};
+  for (int j = 0; j < nseg; ++j) {
+    const int m = (seg_modes >> (4 * j)) & 15;
+    if (seg_rows[j] <= 0 || seg_rows[j] % 128 || m > RWKVQ_EPI_SIGMOID)
+      return RWKVQ_ERR_ARG;
+    rows += seg_rows[j];
+    a.seg_end[j] = rows;
+  }
+  a.x = x; a.y = y; a.M = M; a.N = rows; a.in = in; a.out_per = rows;
+  a.x_ld = x_ld > 0 ? x_ld : (long)nseg * in;
+  if (a.x_ld < (long)nseg * in) return RWKVQ_ERR_ARG;
+  a.mode = RWKVQ_EPI_PER_SEG;
+  a.seg_modes = seg_modes;
+  a.nseg_tab = nseg;
   a.q = reinterpret_cast<const uint8_t*>(w);
   return launch_gemm<F_F16>(a, (hipStream_t)stream);
 }

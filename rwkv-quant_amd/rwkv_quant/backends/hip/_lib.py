@@ -35,6 +35,7 @@ SIGNATURES = {
     "rwkvq_gemm_rtn8": [_P, _P, _I, _I, _I, _P, _L, _P, _I, _I, _P],
     "rwkvq_gemm_f16": [_P, _I, _I, _I, _P, _L, _P, _I, _I, _I, _P],
     "rwkvq_gemv_f16_seg": [_P, _I, _P, _I, _P, _L, _P, _I, _I, _P],
+    "rwkvq_gemm_f16_seg": [_P, _I, _P, _I, _P, _L, _P, _I, _I, _P],
     "rwkvq_dequant_sb6_f32": [_P, _P, _P, _I, _I, _I, _P, _I, _P],
     "rwkvq_dequant_sym_f32": [_P, _P, _P, _P, _I, _I, _I, _P, _I, _P],
     "rwkvq_dequant_rtn8_f32": [_P, _P, _I, _I, _P, _I, _P],

@@ -142,9 +142,10 @@ class _Work:
         self.xs = torch.empty(N, 6, C, **f)      # r, k, v, w, a, g lerps
         self.rkv = torch.empty(N, 3, C, **f)
         self.h = {b: torch.empty(N, r, **f) for b, r in ranks.items()}
-        rp = -(-max(ranks.values()) // 128) * 128
-        # prefill LoRA: the down outputs of all branches, each padded to rp
-        self.h_cat = torch.empty(N, len(ranks) * rp, **f) if N > 8 else None
+        # prefill LoRA: the down outputs of all branches, each padded to a
+        # multiple of 128
+        rp = sum(-(-r // 128) * 128 for r in ranks.values())
+        self.h_cat = torch.empty(N, rp, **f) if N > 8 else None
         self.yl = {b: torch.empty(N, C, **f) for b in ranks}
         self.w = torch.empty(N, C, **f)
         self.kp = torch.empty(N, C, **f)
@@ -259,44 +260,52 @@ class QuantTMix:
         # prefill: the MFMA GEMM over the dense fp16 factors; one launch for
         # the down products of all branches (their lerp slots v, w, a, g are
         # adjacent in wk.xs), one per up product
-        order, rp, A_cat, B_pad, modes = self._prefill_mats()
+        order, rps, A_cat, B_pad, modes = self._prefill_mats()
         xs_flat = wk.xs.view(N, 6 * C)
         s0 = self.SLOT[order[0]]
-        nseg = len(order)
-        _lib.call("rwkvq_gemm_f16", _lib.ptr(A_cat), nseg * rp, C, rp,
+        nseg, tot = len(order), sum(rps)
+        _lib.call("rwkvq_gemm_f16_seg", _lib.ptr(A_cat), nseg,
+                  (ctypes.c_int * nseg)(*rps), C,
                   _lib.ptr(xs_flat[:, s0 * C:]), 6 * C, _lib.ptr(wk.h_cat), N,
-                  _lib.EPI_PER_SEG, modes, _stream())
-        # the down GEMM wrote rows of nseg * rp values
-        hc = wk.h_cat.view(-1)[:N * nseg * rp].view(N, nseg * rp)
+                  modes, _stream())
+        # the down GEMM wrote rows of `tot` values, branch j from column
+        # sum(rps[:j]) on
+        hc = wk.h_cat.view(-1)[:N * tot].view(N, tot)
+        off = 0
         for j, b in enumerate(order):
-            _lib.call("rwkvq_gemm_f16", _lib.ptr(B_pad[b]), C, rp, C,
-                      _lib.ptr(hc[:, j * rp:]), nseg * rp,
-                      _lib.ptr(wk.yl[b]), N, _lib.EPI_STORE, 0, _stream())
+            _lib.call("rwkvq_gemm_f16", _lib.ptr(B_pad[b]), C, rps[j], C,
+                      _lib.ptr(hc[:, off:]), tot, _lib.ptr(wk.yl[b]), N,
+                      _lib.EPI_STORE, 0, _stream())
+            off += rps[j]
 
     def _prefill_mats(self):
         """Prefill LoRA factors padded for the GEMM tiles (built on first
         use): down factors stacked in lerp-slot order (v, w, a, g), each
-        padded with zero rows to rp (a multiple of 128); up factors padded
-        with zero columns to rp.  Padded outputs multiply zero weights."""
+        padded with zero rows to a multiple of 128 (rps); up factors padded
+        with zero columns to the same width.  Padded outputs multiply zero
+        weights."""
         if getattr(self, "_pmats", None) is None:
             order = [b for b in ("v", "w", "a", "g") if b in self.lora]
             C = self.C
-            rp = -(-max(A.shape[0] for A, _ in self.lora.values()) // 128) * 128
+            rps = [-(-self.lora[b][0].shape[0] // 128) * 128 for b in order]
             A0 = self.lora[order[0]][0]
-            A_cat = torch.zeros(len(order) * rp, C, dtype=torch.float16,
+            A_cat = torch.zeros(sum(rps), C, dtype=torch.float16,
                                 device=A0.device)
             B_pad = {}
+            off = 0
             for j, b in enumerate(order):
                 A, Bm = self.lora[b]
                 r = A.shape[0]
-                A_cat[j * rp:j * rp + r] = A
-                Bp = torch.zeros(C, rp, dtype=torch.float16, device=A0.device)
+                A_cat[off:off + r] = A
+                Bp = torch.zeros(C, rps[j], dtype=torch.float16,
+                                 device=A0.device)
                 Bp[:, :r] = Bm
                 B_pad[b] = Bp
+                off += rps[j]
             modes = 0
             for j, b in enumerate(order):
                 modes |= self.EPI_DOWN[b] << (4 * j)
-            self._pmats = (order, rp, A_cat, B_pad, modes)
+            self._pmats = (order, rps, A_cat, B_pad, modes)
         return self._pmats
 
     def run_lora_down(self, wk):

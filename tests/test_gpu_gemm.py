@@ -202,3 +202,40 @@ def test_gemv_f16_segments_errors():
         with pytest.raises(_lib.HipKernelError):
             _lib.call("rwkvq_gemv_f16_seg", _lib.ptr(A), 1, r, 2048,
                       _lib.ptr(x), 2048, yp, n, 0, _lib.stream_handle())
+
+
+@pytest.mark.parametrize("M", [160, 512])
+def test_gemm_f16_segment_table(M):
+    """The prefill LoRA down products in one launch over segments of
+    unequal height (each a multiple of 128): segment j reads input slot j
+    and has its own epilogue; equal, bit for bit, to one launch per
+    segment, and within 2e-5 of the float64 product of the fp16 operands."""
+    import ctypes
+    g = torch.Generator().manual_seed(M)
+    K, rows = 2048, [128, 128, 128, 384]
+    A = [(torch.randn(r, K, generator=g) * 0.05).half() for r in rows]
+    xs = torch.randn(M, 6, K, generator=g)
+    modes = [_lib.EPI_STORE, _lib.EPI_TANH, _lib.EPI_STORE, _lib.EPI_SIGMOID]
+    Ad, xd = torch.cat(A).cuda(), xs.cuda()
+    y = torch.empty(M, sum(rows), device="cuda")
+    sm = sum(m << (4 * j) for j, m in enumerate(modes))
+    _lib.call("rwkvq_gemm_f16_seg", _lib.ptr(Ad), 4,
+              (ctypes.c_int * 4)(*rows), K, _lib.ptr(xd[:, 2]), 6 * K,
+              _lib.ptr(y), M, sm, _lib.stream_handle())
+    fns = {_lib.EPI_STORE: lambda v: v, _lib.EPI_TANH: np.tanh,
+           _lib.EPI_SIGMOID: lambda v: 1 / (1 + np.exp(-v))}
+    off = 0
+    for j, (Aj, m) in enumerate(zip(A, modes)):
+        yj = torch.empty(M, rows[j], device="cuda")
+        _lib.call("rwkvq_gemm_f16", _lib.ptr(Aj.cuda()), rows[j], K, rows[j],
+                  _lib.ptr(xd[:, 2 + j]), 6 * K, _lib.ptr(yj), M, m, 0,
+                  _lib.stream_handle())
+        assert torch.equal(y[:, off:off + rows[j]], yj), j
+        ref = fns[m](xs[:, 2 + j].half().double().numpy()
+                     @ Aj.double().numpy().T)
+        assert relmax(y[:, off:off + rows[j]].cpu().numpy(), ref) < 2e-5
+        off += rows[j]
+    with pytest.raises(_lib.HipKernelError):      # a segment off the tiles
+        _lib.call("rwkvq_gemm_f16_seg", _lib.ptr(Ad), 2,
+                  (ctypes.c_int * 2)(100, 668), K, _lib.ptr(xd[:, 2]),
+                  6 * K, _lib.ptr(y), M, 0, _lib.stream_handle())
