@@ -112,6 +112,16 @@ int rwkvq_gemm_rtn8(const int8_t* codes, const uint16_t* scale, int rows,
                     int in, int out_per, const float* x, long x_ld, float* y,
                     int M, int epilogue, void* stream);
 
+/* Split-K workspace of the GEMMs on the current device: ws (16-byte
+ * aligned, ws_bytes) holds partial output tiles, counters[n_counters]
+ * (int32, zero when registered) count the workgroups that finished a tile;
+ * every launch leaves the counters at zero again.  Without a workspace
+ * (the default, or ws == NULL) no GEMM splits K.  Launches that use it
+ * must not overlap (one stream at a time).  No counterpart in the
+ * reference (its matmul library keeps its own scratch). */
+int rwkvq_gemm_workspace(void* ws, long ws_bytes, int* counters,
+                         int n_counters);
+
 /* The same GEMM over dense fp16 rows W [rows, in] (in % 128 == 0): the
  * prefill LoRA products.  With epilogue RWKVQ_EPI_PER_SEG each input
  * segment j (rows j*out_per ..) applies the mode in bits 4j..4j+3 of

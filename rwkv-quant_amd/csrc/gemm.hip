@@ -60,6 +60,11 @@ struct GemmArgs {
   // [seg_end[j-1], seg_end[j]) and reads x at x + j * in; 0 = uniform
   int nseg_tab;
   int seg_end[8];
+  // split-K: `split` workgroups share an output tile, each taking an equal
+  // run of the K steps; partial tiles go to ws, cnt[tile] counts arrivals
+  int split;
+  float* ws;
+  int* cnt;
 };
 
 constexpr int kStepK = 128;                 // columns per K step
@@ -179,15 +184,18 @@ gemm_kernel(GemmArgs a) {
   // M tiles of one N tile go to the same XCD back to back, so that XCD's L2
   // serves the W tile to all of them after one HBM read; N tiles are dealt
   // across the XCDs.
-  int nt, mt;
-  if ((a.nt & 7) == 0) {
+  // With split-K, index j = nt * split + sp stands in for nt: the M tiles
+  // of one (N tile, K run) share an XCD, the runs of a tile spread out.
+  int j, mt;
+  if (((a.nt * a.split) & 7) == 0) {
     const int slot = blockIdx.x >> 3;
     mt = slot % a.mt;
-    nt = (slot / a.mt) * 8 + (blockIdx.x & 7);
+    j = (slot / a.mt) * 8 + (blockIdx.x & 7);
   } else {
     mt = blockIdx.x % a.mt;
-    nt = blockIdx.x / a.mt;
+    j = blockIdx.x / a.mt;
   }
+  const int nt = j / a.split, sp = j % a.split;
   const int n0 = nt * BN;
   const int m0 = mt * BM;
   int seg = n0 / a.out_per;
@@ -198,7 +206,8 @@ gemm_kernel(GemmArgs a) {
       seg += (j + 1 < a.nseg_tab && n0 >= a.seg_end[j]) ? 1 : 0;
   }
   const int ng = a.in >> 5, nsb = a.in >> 8;
-  const int nsteps = a.in / kStepK;
+  const int nrun = a.in / kStepK / a.split;   // K steps of this workgroup
+  const int c0 = sp * nrun;
   const float* xb = a.x + (size_t)seg * a.in;
 
   // ---- x staging: item = (token, group of the step, sub-step)
@@ -246,16 +255,16 @@ gemm_kernel(GemmArgs a) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[mi][ni][v] = 0.f;
 
-  load_w(kg, cur);
-  load_x(kg);
+  load_w(c0 + kg, cur);
+  load_x(c0 + kg);
   store_x(0);
   __syncthreads();
 
-  const int nsg = nsteps / KG;                 // steps of each group
+  const int nsg = nrun / KG;                   // steps of each group
   for (int i = 0; i < nsg; ++i) {
-    const int c = i * KG + kg;
+    const int c = c0 + i * KG + kg;
     // clamped to the group's last step: loads stay in W / x
-    const int cn = min(c + KG, nsteps - KG + kg);
+    const int cn = min(c + KG, c0 + nrun - KG + kg);
     load_w(cn, nxt);
     load_x(cn);
     // keep the loads of step c + KG ahead of this step's MFMAs: left to
@@ -317,15 +326,101 @@ gemm_kernel(GemmArgs a) {
                 acc[mi][ni][v];
     }
     __syncthreads();
-    if (kg == 1) return;
+    if (kg == 0) {
 #pragma unroll
-    for (int mi = 0; mi < WM; ++mi)
+      for (int mi = 0; mi < WM; ++mi)
 #pragma unroll
-      for (int ni = 0; ni < WN; ++ni)
+        for (int ni = 0; ni < WN; ++ni)
 #pragma unroll
-        for (int v = 0; v < 16; ++v)
-          acc[mi][ni][v] += red[(wave * NA + (mi * WN + ni) * 16 + v) * 64 + lane];
+          for (int v = 0; v < 16; ++v)
+            acc[mi][ni][v] += red[(wave * NA + (mi * WN + ni) * 16 + v) * 64 + lane];
+    }
   }
+
+  if (a.split > 1) {
+    // Every run stores its partial tile (lane-major, coalesced) and counts
+    // itself in; the last to arrive adds the partials in run order 0, 1,
+    // ... (the same sum whichever run finishes last), applies the
+    // epilogue and re-arms the counter for the next launch.  Partials and
+    // counter move by agent-scope relaxed atomics, which are coherent
+    // across the XCDs' L2s by themselves; a device-scope fence instead
+    // would write back and invalidate the whole L2 in every workgroup.
+    constexpr int NA = WM * WN * 16;
+    constexpr int TE = 4 * NA * 64;            // floats per partial tile
+    const int tile = nt * a.mt + mt;
+    float* part = a.ws + (size_t)tile * a.split * TE;
+    if (kg == 0) {
+#pragma unroll
+      for (int mi = 0; mi < WM; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < WN; ++ni)
+#pragma unroll
+          for (int v = 0; v < 16; ++v)
+            __hip_atomic_store(
+                part + (size_t)sp * TE +
+                    (wave * NA + (mi * WN + ni) * 16 + v) * 64 + lane,
+                acc[mi][ni][v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __shared__ int s_last;
+    // this wave's partial stores are complete before the barrier, so all
+    // of them are before the count goes up
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0)
+      s_last = __hip_atomic_fetch_add(a.cnt + tile, 1, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT) ==
+               a.split - 1;
+    __syncthreads();
+    if (!s_last) return;
+    if (kg == 0) {
+      float sum[WM][WN][16];
+#pragma unroll
+      for (int mi = 0; mi < WM; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < WN; ++ni)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) sum[mi][ni][v] = 0.f;
+      for (int q = 0; q < a.split; ++q) {
+        if (q == sp) {                         // (uniform branch)
+#pragma unroll
+          for (int mi = 0; mi < WM; ++mi)
+#pragma unroll
+            for (int ni = 0; ni < WN; ++ni)
+#pragma unroll
+              for (int v = 0; v < 16; ++v) sum[mi][ni][v] += acc[mi][ni][v];
+          continue;
+        }
+        // one run's partial tile at a time: all its loads in flight at once
+        float p[WM][WN][16];
+        const float* pq = part + (size_t)q * TE + wave * NA * 64 + lane;
+#pragma unroll
+        for (int mi = 0; mi < WM; ++mi)
+#pragma unroll
+          for (int ni = 0; ni < WN; ++ni)
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+              p[mi][ni][v] = __hip_atomic_load(
+                  pq + ((mi * WN + ni) * 16 + v) * 64, __ATOMIC_RELAXED,
+                  __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int mi = 0; mi < WM; ++mi)
+#pragma unroll
+          for (int ni = 0; ni < WN; ++ni)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) sum[mi][ni][v] += p[mi][ni][v];
+      }
+#pragma unroll
+      for (int mi = 0; mi < WM; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < WN; ++ni)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) acc[mi][ni][v] = sum[mi][ni][v];
+      if (threadIdx.x == 0)
+        __hip_atomic_store(a.cnt + tile, 0, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  if (kg != 0) return;
 
   // ---- epilogue: lane holds tokens m0 + 32 mi + r, rows 4 at a time
   const int mode = a.mode == RWKVQ_EPI_PER_SEG
@@ -377,34 +472,78 @@ gemm_kernel(GemmArgs a) {
 #ifndef RWKVQ_GEMM_KG
 #define RWKVQ_GEMM_KG 2
 #endif
+#ifndef RWKVQ_GEMM_SPLIT
+#define RWKVQ_GEMM_SPLIT 1
+#endif
+// split-K: runs of >= kMinRun steps, until the launch has >= RWKVQ_SPLIT_WGS
+// workgroups (the 128 x 128 tile is used from that count on)
+#ifndef RWKVQ_SPLIT_WGS
+#define RWKVQ_SPLIT_WGS 192
+#endif
+constexpr int kMinRun = 8;
+
+// Split-K workspace registered by the caller (rwkvq_gemm_workspace), one
+// per device.
+struct SplitWs {
+  float* ws;
+  long bytes;
+  int* cnt;
+  int ncnt;
+};
+SplitWs g_split_ws[64];
+
+const SplitWs* current_ws() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  return g_split_ws[dev].ws ? &g_split_ws[dev] : nullptr;
+}
 
 // Two K groups (8 waves) wherever the tile's registers allow two waves per
 // SIMD (all tiles but 256 x 128) and the step count is even.
 template <int FMT, int WN, int WM>
-int launch_tile(const GemmArgs& a, hipStream_t s) {
+int launch_tile(const GemmArgs& a, hipStream_t s, int split = 1,
+                const SplitWs* ws = nullptr) {
   GemmArgs b = a;
   b.nt = a.N / (128 * WN);
   b.mt = (a.M + 32 * WM - 1) / (32 * WM);
+  b.split = split;
+  if (split > 1) { b.ws = ws->ws; b.cnt = ws->cnt; }
+  const int grid = b.nt * b.mt * split;
   constexpr bool two = RWKVQ_GEMM_KG == 2 && WN * WM <= 4;
-  if (two && (a.in / kStepK) % 2 == 0)
-    hipLaunchKernelGGL((gemm_kernel<FMT, WN, WM, two ? 2 : 1>),
-                       dim3(b.nt * b.mt), dim3(512), 0, s, b);
+  if (two && (a.in / kStepK / split) % 2 == 0)
+    hipLaunchKernelGGL((gemm_kernel<FMT, WN, WM, two ? 2 : 1>), dim3(grid),
+                       dim3(512), 0, s, b);
   else
-    hipLaunchKernelGGL((gemm_kernel<FMT, WN, WM, 1>), dim3(b.nt * b.mt),
-                       dim3(256), 0, s, b);
+    hipLaunchKernelGGL((gemm_kernel<FMT, WN, WM, 1>), dim3(grid), dim3(256),
+                       0, s, b);
   return hipGetLastError() == hipSuccess ? RWKVQ_OK : RWKVQ_ERR_LAUNCH;
 }
 
-// Largest tile that still gives >= 256 workgroups (one per CU); N tiles of
-// 256 rows need out_per % 256 == 0.
+// Tile choice: 256 x 128 (a wave: 64 rows x 128 tokens) where that alone
+// gives >= 256 workgroups; else 128 x 128 (a wave: 32 rows x 128 tokens,
+// each decoded weight feeds 4 MFMAs), split along K where that fills the
+// chip; else the largest smaller tile that still gives >= 256 workgroups.
+// N tiles of 256 rows need out_per % 256 == 0; segment tables take 128-row
+// tiles (their segments are multiples of 128 rows).
 template <int FMT>
 int launch_gemm(const GemmArgs& a, hipStream_t s) {
   auto wgs = [&](int bn, int bm) {
     return (long)(a.N / bn) * ((a.M + bm - 1) / bm);
   };
-  // (segment tables: 128-row tiles, segments are multiples of 128 rows)
+  const int nsteps = a.in / kStepK;
   const bool wide = a.out_per % 256 == 0 && a.nseg_tab == 0;
   if (wide && wgs(256, 128) >= 256) return launch_tile<FMT, 2, 4>(a, s);
+  if (RWKVQ_GEMM_SPLIT && a.M > 64 && nsteps % 2 == 0) {
+    const long t = wgs(128, 128);
+    const SplitWs* ws = current_ws();
+    int split = 1;
+    while (t * split < RWKVQ_SPLIT_WGS && split < 8 &&
+           nsteps % (2 * kMinRun * split) == 0 && ws && t <= ws->ncnt &&
+           t * 2 * split * 128 * 128 * (long)sizeof(float) <= ws->bytes)
+      split *= 2;
+    if (t * split >= RWKVQ_SPLIT_WGS)
+      return launch_tile<FMT, 1, 4>(a, s, split, ws);
+  }
   if (wide && wgs(256, 64) >= 256) return launch_tile<FMT, 2, 2>(a, s);
   if (wgs(128, 64) >= 256) return launch_tile<FMT, 1, 2>(a, s);
   return launch_tile<FMT, 1, 1>(a, s);
@@ -423,6 +562,7 @@ int check_gemm(int rows, int in, int out_per, int M, long x_ld, int mode,
 GemmArgs make_args(int rows, int in, int out_per, const float* x, long x_ld,
                    float* y, int M, int mode) {
   GemmArgs a{};
+  a.split = 1;
   a.x = x; a.y = y; a.M = M; a.N = rows; a.in = in; a.out_per = out_per;
   a.mode = mode;
   a.x_ld = x_ld > 0 ? x_ld : (long)(rows / out_per) * in;
@@ -432,6 +572,23 @@ GemmArgs make_args(int rows, int in, int out_per, const float* x, long x_ld,
 }  // namespace
 
 extern "C" {
+
+int rwkvq_gemm_workspace(void* ws, long ws_bytes, int* counters,
+                         int n_counters) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+    return RWKVQ_ERR_ARG;
+  if (!ws || !counters) {
+    g_split_ws[dev] = SplitWs{nullptr, 0, nullptr, 0};
+    return RWKVQ_OK;
+  }
+  if (ws_bytes <= 0 || n_counters <= 0 ||
+      reinterpret_cast<uintptr_t>(ws) % 16)
+    return RWKVQ_ERR_ARG;
+  g_split_ws[dev] = SplitWs{static_cast<float*>(ws), ws_bytes, counters,
+                            n_counters};
+  return RWKVQ_OK;
+}
 
 int rwkvq_gemm_sb6(const uint8_t* nib, const uint32_t* hb, const uint8_t* rec,
                    int bits, int rows, int in, int out_per, const float* x,
@@ -497,6 +654,7 @@ int rwkvq_gemm_f16_seg(const uint16_t* w, int nseg, const int* seg_rows,
     return RWKVQ_ERR_ARG;
   int rows = 0;
   GemmArgs a{};
+  a.split = 1;
   for (int j = 0; j < nseg; ++j) {
     const int m = (seg_modes >> (4 * j)) & 15;
     if (seg_rows[j] <= 0 || seg_rows[j] % 128 || m > RWKVQ_EPI_SIGMOID)

@@ -36,6 +36,7 @@ SIGNATURES = {
     "rwkvq_gemm_f16": [_P, _I, _I, _I, _P, _L, _P, _I, _I, _I, _P],
     "rwkvq_gemv_f16_seg": [_P, _I, _P, _I, _P, _L, _P, _I, _I, _P],
     "rwkvq_gemm_f16_seg": [_P, _I, _P, _I, _P, _L, _P, _I, _I, _P],
+    "rwkvq_gemm_workspace": [_P, _L, _P, _I],
     "rwkvq_dequant_sb6_f32": [_P, _P, _P, _I, _I, _I, _P, _I, _P],
     "rwkvq_dequant_sym_f32": [_P, _P, _P, _P, _I, _I, _I, _P, _I, _P],
     "rwkvq_dequant_rtn8_f32": [_P, _P, _I, _I, _P, _I, _P],
@@ -85,8 +86,36 @@ def load():
     return lib
 
 
+# split-K workspace of the GEMMs: partial tiles + arrival counters (zeroed
+# once; every launch leaves them at zero)
+GEMM_WS_BYTES = 64 << 20
+GEMM_WS_COUNTERS = 8192
+_gemm_ws = {}
+
+
+def ensure_gemm_workspace():
+    """Register the GEMM split-K workspace of the current device once
+    (eagerly: never from inside a stream capture, where the GEMMs then run
+    without splitting)."""
+    import torch
+    dev = torch.cuda.current_device()
+    if dev in _gemm_ws or torch.cuda.is_current_stream_capturing():
+        return
+    ws = torch.empty(GEMM_WS_BYTES, dtype=torch.uint8, device=f"cuda:{dev}")
+    cnt = torch.zeros(GEMM_WS_COUNTERS, dtype=torch.int32,
+                      device=f"cuda:{dev}")
+    torch.cuda.synchronize(dev)
+    st = load().rwkvq_gemm_workspace(ptr(ws), GEMM_WS_BYTES, ptr(cnt),
+                                     GEMM_WS_COUNTERS)
+    if st != RWKVQ_OK:
+        raise HipKernelError(f"rwkvq_gemm_workspace: status {st}")
+    _gemm_ws[dev] = (ws, cnt)
+
+
 def call(name, *args):
     """Invoke an entry point; a non-zero status raises HipKernelError."""
+    if name.startswith("rwkvq_gemm_") and name != "rwkvq_gemm_workspace":
+        ensure_gemm_workspace()
     st = getattr(load(), name)(*args)
     if st != RWKVQ_OK:
         raise HipKernelError(f"{name}: status {st} "
