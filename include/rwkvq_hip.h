@@ -51,6 +51,22 @@ extern "C" {
 #define RWKVQ_EPI_PER_SEG 5  /* rwkvq_gemm_f16: mode of segment j in bits
                                 4j..4j+3 of seg_modes */
 
+/* GEMM flags, or-ed into the epilogue of rwkvq_gemm_*:
+ *   RWKVQ_X_F16  x is fp16 in the pair order of the weight format
+ *                (rwkvq_x16), x_ld in halves;
+ *   RWKVQ_Y_F16 | (order << RWKVQ_Y_ORDER_SHIFT)  y is written as fp16
+ *                [M, rows] in pair order `order` (the input of a GEMM over
+ *                a format of that order); not with RWKVQ_EPI_ADD. */
+#define RWKVQ_X_F16 16
+#define RWKVQ_Y_F16 32
+#define RWKVQ_Y_ORDER_SHIFT 6
+/* Pair orders of fp16 GEMM inputs: within each 32-column group, halves
+ * 2i, 2i+1 hold columns (c0(i), c1(i)) -- the order in which the format's
+ * decoder pairs its weights. */
+#define RWKVQ_ORDER_PAIRS 0  /* (2i, 2i+1): sym8, rtn8, dense fp16 */
+#define RWKVQ_ORDER_SB6 1    /* (i, i+16): sb6 int4/5/6 */
+#define RWKVQ_ORDER_SYM6 2   /* (i, i+8) for i < 8, (i+8, i+16) else: sym6 */
+
 /* ---------------------------------------------------------------- GEMV
  * y[n, r] = epi( sum_c x[n, r / out_per, c] * W[r, c] ),  n < n_cols.
  * x is fp32 with element (n, seg, c) at x[n * x_ld + seg * IN + c]
@@ -111,6 +127,14 @@ int rwkvq_gemm_sym(const uint8_t* codes, const uint32_t* hb, const int8_t* qs,
 int rwkvq_gemm_rtn8(const int8_t* codes, const uint16_t* scale, int rows,
                     int in, int out_per, const float* x, long x_ld, float* y,
                     int M, int epilogue, void* stream);
+
+/* fp32 x [M, x_ld] -> fp16 out [M, out_ld] (round to nearest even), the
+ * first `cols` columns (a multiple of 32) in pair order `order`
+ * (RWKVQ_ORDER_*): the GEMMs' RWKVQ_X_F16 input.  x, out 16-byte aligned,
+ * x_ld % 4 == 0, out_ld % 8 == 0.  No counterpart in the reference (its
+ * matmul rounds x to fp16 itself: x.astype(mx.float16)). */
+int rwkvq_x16(const float* x, long x_ld, int cols, int M, int order,
+              uint16_t* out, long out_ld, void* stream);
 
 /* Split-K workspace of the GEMMs on the current device: ws (16-byte
  * aligned, ws_bytes) holds partial output tiles, counters[n_counters]
@@ -200,6 +224,13 @@ int rwkvq_shift_lerp(const float* x, const float* ln_w, const float* ln_b,
                      const float* prev, const float* coef, int ncoef,
                      float* out, float* new_prev, int B, int T, int D,
                      void* stream);
+/* The same with fp16 out [B*T, ncoef, D] (round to nearest even), each
+ * 32-column group in pair order `order` (RWKVQ_ORDER_*): the RWKVQ_X_F16
+ * input of the prefill GEMMs.  D % 32 == 0, out 16-byte aligned. */
+int rwkvq_shift_lerp_f16(const float* x, const float* ln_w, const float* ln_b,
+                         const float* prev, const float* coef, int ncoef,
+                         uint16_t* out, int order, float* new_prev, int B,
+                         int T, int D, void* stream);
 
 /* Per-channel WKV inputs from rkv [N, 3, D] and the LoRA outputs yw, ya,
  * yv (NULL on layer 0) [N, D]: w = exp(-0.606531 * sigmoid(yw + w0)),
@@ -253,6 +284,12 @@ int rwkvq_wkv_tail(const float* y, const float* rkv, const float* kp,
                    const float* vp, const float* g, const float* r_k,
                    const float* ln_w, const float* ln_b, float* out, int N,
                    int D, int head_size, void* stream);
+/* The same with fp16 out [N, D] in pair order `order` (RWKVQ_ORDER_*): the
+ * RWKVQ_X_F16 input of the output projection's GEMM. */
+int rwkvq_wkv_tail_f16(const float* y, const float* rkv, const float* kp,
+                       const float* vp, const float* g, const float* r_k,
+                       const float* ln_w, const float* ln_b, uint16_t* out,
+                       int order, int N, int D, int head_size, void* stream);
 
 /* Decode (T = 1) time-mix core in one launch per (sequence, head):
  * rwkvq_wkv_prep + one rwkvq_wkv7_scan step + rwkvq_wkv_tail for
@@ -290,12 +327,13 @@ int rwkvq_wkv7_decode_lora(const float* rkv, const float* const* h,
  * multiple of 128) of one matrix w [sum rows, in]: segment j reads
  * x[t * x_ld + j * in + c] and writes columns [sum_{i<j} rows_i, ...) of
  * y [M, sum rows] with epilogue field j of seg_modes.  in % 128 == 0.
+ * flags: RWKVQ_X_F16 / RWKVQ_Y_F16 as for rwkvq_gemm_f16 (0: fp32 x, y).
  * Replaces: the down products of QuantTMix._lora in prefill, all
  * branches in one launch, each padded only to 128 rows (reference:
  * quant_model.py:462-526). */
 int rwkvq_gemm_f16_seg(const uint16_t* w, int nseg, const int* seg_rows,
                        int in, const float* x, long x_ld, float* y, int M,
-                       int seg_modes, void* stream);
+                       int seg_modes, int flags, void* stream);
 
 /* Dense fp16 rows in up to 8 segments of one matrix w [sum rows, in], for
  * 1..16 input rows, on the matrix cores: segment j (rows seg_rows[j], a

@@ -65,6 +65,8 @@ struct GemmArgs {
   int split;
   float* ws;
   int* cnt;
+  int xh;                // x is fp16 in the format's pair order
+  int yord;              // -1: fp32 y; else fp16 y in pair order yord
 };
 
 constexpr int kStepK = 128;                 // columns per K step
@@ -164,7 +166,7 @@ __device__ __forceinline__ void weights_of(const Raw2& r2, int gi, int kb,
   }
 }
 
-template <int FMT, int WN, int WM, int KG>
+template <int FMT, int WN, int WM, int KG, bool XH>
 __global__ void __launch_bounds__(256 * KG)
 gemm_kernel(GemmArgs a) {
   constexpr int BM = 32 * WM;
@@ -209,20 +211,27 @@ gemm_kernel(GemmArgs a) {
   const int nrun = a.in / kStepK / a.split;   // K steps of this workgroup
   const int c0 = sp * nrun;
   const float* xb = a.x + (size_t)seg * a.in;
+  // fp16 x (XH): already in pair order, x_ld in halves
+  const uint16_t* xh = reinterpret_cast<const uint16_t*>(a.x) + (size_t)seg * a.in;
 
   // ---- x staging: item = (token, group of the step, sub-step)
-  float4 xa[XI], xbv[XI];
+  float4 xa[XH ? 1 : XI], xbv[XH ? 1 : XI];
+  uint4 xq[XH ? XI : 1];
   auto load_x = [&](int c) {
 #pragma unroll
     for (int p = 0; p < XI; ++p) {
       const int it = tid + 256 * p;
       const int t = min(m0 + (it >> 4), a.M - 1);
-      const int gq = (it >> 2) & 3, s = it & 3;
-      int ca, cb;
-      step_cols<FMT>(s, ca, cb);
-      const float* src = xb + (size_t)t * a.x_ld + c * kStepK + gq * 32;
-      xa[p] = *reinterpret_cast<const float4*>(src + ca);
-      xbv[p] = *reinterpret_cast<const float4*>(src + cb);
+      if constexpr (XH) {
+        xq[p] = ld16(xh + (size_t)t * a.x_ld + c * kStepK + (it & 15) * 8);
+      } else {
+        const int gq = (it >> 2) & 3, s = it & 3;
+        int ca, cb;
+        step_cols<FMT>(s, ca, cb);
+        const float* src = xb + (size_t)t * a.x_ld + c * kStepK + gq * 32;
+        xa[p] = *reinterpret_cast<const float4*>(src + ca);
+        xbv[p] = *reinterpret_cast<const float4*>(src + cb);
+      }
     }
   };
   auto store_x = [&](int buf) {
@@ -231,7 +240,7 @@ gemm_kernel(GemmArgs a) {
       const int it = tid + 256 * p;
       const int tl = it >> 4, gq = (it >> 2) & 3, s = it & 3;
       *reinterpret_cast<uint4*>(&sx[kg][buf][tl * kRowH + gq * 32 + s * 8]) =
-          x_pairs<FMT>(xa[p], xbv[p]);
+          XH ? xq[p] : x_pairs<FMT>(xa[p], xbv[p]);
     }
   };
 
@@ -299,7 +308,10 @@ gemm_kernel(GemmArgs a) {
     // the prefetched registers are consumed only from here on
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int p = 0; p < XI; ++p) { pin(xa[p]); pin(xbv[p]); }
+    for (int p = 0; p < XI; ++p) {
+      if constexpr (XH) pin(xq[p]);
+      else { pin(xa[p]); pin(xbv[p]); }
+    }
 #pragma unroll
     for (int ni = 0; ni < WN; ++ni) pin_raw2<FMT>(nxt[ni]);
     store_x((i + 1) & 1);
@@ -423,6 +435,7 @@ gemm_kernel(GemmArgs a) {
   if (kg != 0) return;
 
   // ---- epilogue: lane holds tokens m0 + 32 mi + r, rows 4 at a time
+  // (rows 8 q + 4 h + e of each 32-row block in acc[.][.][4 q + e])
   const int mode = a.mode == RWKVQ_EPI_PER_SEG
                        ? (a.seg_modes >> (4 * seg)) & 15 : a.mode;
 #pragma unroll
@@ -431,10 +444,12 @@ gemm_kernel(GemmArgs a) {
     if (t >= a.M) continue;
     float* yrow = a.y + (size_t)t * a.N;
 #pragma unroll
-    for (int ni = 0; ni < WN; ++ni)
+    for (int ni = 0; ni < WN; ++ni) {
+      const int nb = n0 + wave * 32 * WN + ni * 32;   // 32-row block
+      float4 v4[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int n = n0 + wave * 32 * WN + ni * 32 + 8 * q + 4 * h;
+        const int n = nb + 8 * q + 4 * h;
         float4 v = make_float4(acc[mi][ni][4 * q], acc[mi][ni][4 * q + 1],
                                acc[mi][ni][4 * q + 2], acc[mi][ni][4 * q + 3]);
         if (FMT == F_RTN8) {
@@ -444,10 +459,9 @@ gemm_kernel(GemmArgs a) {
           v.z *= f16_bits_to_f32(sc.y & 0xFFFFu);
           v.w *= f16_bits_to_f32(sc.y >> 16);
         }
-        float4* yp = reinterpret_cast<float4*>(yrow + n);
         switch (mode) {
           case RWKVQ_EPI_ADD: {
-            const float4 o = *yp;
+            const float4 o = *reinterpret_cast<const float4*>(yrow + n);
             v.x += o.x; v.y += o.y; v.z += o.z; v.w += o.w;
             break;
           }
@@ -464,8 +478,42 @@ gemm_kernel(GemmArgs a) {
             break;
           default: break;
         }
-        *yp = v;
+        v4[q] = v;
       }
+      if (a.yord < 0) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          *reinterpret_cast<float4*>(yrow + nb + 8 * q + 4 * h) = v4[q];
+        continue;
+      }
+      // fp16 output in the pair order of the consuming GEMM: the block's 32
+      // rows are that GEMM's 32-column group, half 2i / 2i+1 = columns
+      // (c0(i), c1(i)); a lane's rows pair up with rows it holds itself
+      uint16_t* yh = reinterpret_cast<uint16_t*>(a.y) + (size_t)t * a.N + nb;
+      // rounded to fp32 first, as the fp32 output (no fused mixed-precision
+      // multiply-add + conversion)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) pin(v4[q]);
+      auto h2 = [](float lo, float hi) { return pack_h2(lo, hi); };
+      if (a.yord == RWKVQ_ORDER_PAIRS) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          *reinterpret_cast<uint2*>(yh + 8 * q + 4 * h) =
+              make_uint2(h2(v4[q].x, v4[q].y), h2(v4[q].z, v4[q].w));
+      } else {
+        // sb6: (c, c + 16) = rows of q and q + 2; sym6: (c, c + 8) = rows
+        // of q and q + 1, c in [0, 8) or [16, 24)
+        const bool sb = a.yord == RWKVQ_ORDER_SB6;
+        const float4 l0 = v4[0], p0 = sb ? v4[2] : v4[1];
+        const float4 l1 = sb ? v4[1] : v4[2], p1 = v4[3];
+        *reinterpret_cast<uint4*>(yh + 8 * h) =
+            make_uint4(h2(l0.x, p0.x), h2(l0.y, p0.y), h2(l0.z, p0.z),
+                       h2(l0.w, p0.w));
+        *reinterpret_cast<uint4*>(yh + 16 + 8 * h) =
+            make_uint4(h2(l1.x, p1.x), h2(l1.y, p1.y), h2(l1.z, p1.z),
+                       h2(l1.w, p1.w));
+      }
+    }
   }
 }
 
@@ -510,12 +558,22 @@ int launch_tile(const GemmArgs& a, hipStream_t s, int split = 1,
   if (split > 1) { b.ws = ws->ws; b.cnt = ws->cnt; }
   const int grid = b.nt * b.mt * split;
   constexpr bool two = RWKVQ_GEMM_KG == 2 && WN * WM <= 4;
-  if (two && (a.in / kStepK / split) % 2 == 0)
-    hipLaunchKernelGGL((gemm_kernel<FMT, WN, WM, two ? 2 : 1>), dim3(grid),
-                       dim3(512), 0, s, b);
-  else
-    hipLaunchKernelGGL((gemm_kernel<FMT, WN, WM, 1>), dim3(grid), dim3(256),
-                       0, s, b);
+  constexpr int KG2 = two ? 2 : 1;
+  if (two && (a.in / kStepK / split) % 2 == 0) {
+    if (a.xh)
+      hipLaunchKernelGGL((gemm_kernel<FMT, WN, WM, KG2, true>), dim3(grid),
+                         dim3(512), 0, s, b);
+    else
+      hipLaunchKernelGGL((gemm_kernel<FMT, WN, WM, KG2, false>), dim3(grid),
+                         dim3(512), 0, s, b);
+  } else {
+    if (a.xh)
+      hipLaunchKernelGGL((gemm_kernel<FMT, WN, WM, 1, true>), dim3(grid),
+                         dim3(256), 0, s, b);
+    else
+      hipLaunchKernelGGL((gemm_kernel<FMT, WN, WM, 1, false>), dim3(grid),
+                         dim3(256), 0, s, b);
+  }
   return hipGetLastError() == hipSuccess ? RWKVQ_OK : RWKVQ_ERR_LAUNCH;
 }
 
@@ -551,6 +609,14 @@ int launch_gemm(const GemmArgs& a, hipStream_t s) {
 
 int check_gemm(int rows, int in, int out_per, int M, long x_ld, int mode,
                int k_mult = 256) {
+  if (mode & ~(15 | RWKVQ_X_F16 | RWKVQ_Y_F16 | (3 << RWKVQ_Y_ORDER_SHIFT)))
+    return RWKVQ_ERR_ARG;
+  if (mode & RWKVQ_Y_F16) {                   // fp16 y: no residual add
+    if (((mode >> RWKVQ_Y_ORDER_SHIFT) & 3) > RWKVQ_ORDER_SYM6 ||
+        (mode & 15) == RWKVQ_EPI_ADD)
+      return RWKVQ_ERR_ARG;
+  }
+  mode &= 15;
   if (rows <= 0 || in <= 0 || M <= 0 || out_per <= 0) return RWKVQ_ERR_ARG;
   if (in % k_mult) return RWKVQ_ERR_ARG;
   if (rows % out_per || out_per % 128) return RWKVQ_ERR_ARG;
@@ -559,19 +625,69 @@ int check_gemm(int rows, int in, int out_per, int M, long x_ld, int mode,
   return RWKVQ_OK;
 }
 
+// x rows are read 16 bytes at a time
+int check_x(const void* x, long x_ld, int xh) {
+  if (reinterpret_cast<uintptr_t>(x) % 16 || x_ld % (xh ? 8 : 4))
+    return RWKVQ_ERR_ARG;
+  return RWKVQ_OK;
+}
+
 GemmArgs make_args(int rows, int in, int out_per, const float* x, long x_ld,
                    float* y, int M, int mode) {
   GemmArgs a{};
   a.split = 1;
+  a.xh = (mode & RWKVQ_X_F16) != 0;
+  a.yord = (mode & RWKVQ_Y_F16) ? (mode >> RWKVQ_Y_ORDER_SHIFT) & 3 : -1;
+  mode &= 15;
   a.x = x; a.y = y; a.M = M; a.N = rows; a.in = in; a.out_per = out_per;
   a.mode = mode;
   a.x_ld = x_ld > 0 ? x_ld : (long)(rows / out_per) * in;
   return a;
 }
 
+// fp32 x -> fp16 x in the pair order of a weight format: thread = one
+// 8-half chunk (token t, 32-column group, sub-step s) of the GEMM's LDS rows.
+template <int FMT>
+__global__ void __launch_bounds__(256)
+x16_kernel(const float* __restrict__ x, long x_ld, uint16_t* __restrict__ out,
+           long out_ld, int M, int cols) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  const int per = cols >> 3;                  // chunks per token
+  if (i >= (long)M * per) return;
+  const int t = (int)(i / per), c = (int)(i % per);
+  const int g = c >> 2, s = c & 3;
+  int ca, cb;
+  step_cols<FMT>(s, ca, cb);
+  const float* src = x + (size_t)t * x_ld + g * 32;
+  const uint4 v = x_pairs<FMT>(*reinterpret_cast<const float4*>(src + ca),
+                               *reinterpret_cast<const float4*>(src + cb));
+  *reinterpret_cast<uint4*>(out + (size_t)t * out_ld + c * 8) = v;
+}
+
 }  // namespace
 
 extern "C" {
+
+int rwkvq_x16(const float* x, long x_ld, int cols, int M, int order,
+              uint16_t* out, long out_ld, void* stream) {
+  if (!x || !out || M <= 0 || cols <= 0 || cols % 32 || x_ld < cols ||
+      out_ld < cols || check_x(x, x_ld, 0) || check_x(out, out_ld, 1) ||
+      order < 0 || order > 2)
+    return RWKVQ_ERR_ARG;
+  const long n = (long)M * (cols / 8);
+  const dim3 grid((unsigned)((n + 255) / 256));
+  hipStream_t s = (hipStream_t)stream;
+  if (order == RWKVQ_ORDER_PAIRS)
+    hipLaunchKernelGGL(x16_kernel<F_SYM8>, grid, dim3(256), 0, s, x, x_ld,
+                       out, out_ld, M, cols);
+  else if (order == RWKVQ_ORDER_SB6)
+    hipLaunchKernelGGL(x16_kernel<F_SB6_4>, grid, dim3(256), 0, s, x, x_ld,
+                       out, out_ld, M, cols);
+  else
+    hipLaunchKernelGGL(x16_kernel<F_SYM6>, grid, dim3(256), 0, s, x, x_ld,
+                       out, out_ld, M, cols);
+  return hipGetLastError() == hipSuccess ? RWKVQ_OK : RWKVQ_ERR_LAUNCH;
+}
 
 int rwkvq_gemm_workspace(void* ws, long ws_bytes, int* counters,
                          int n_counters) {
@@ -595,6 +711,7 @@ int rwkvq_gemm_sb6(const uint8_t* nib, const uint32_t* hb, const uint8_t* rec,
                    long x_ld, float* y, int M, int mode, void* stream) {
   GemmArgs a = make_args(rows, in, out_per, x, x_ld, y, M, mode);
   int st = check_gemm(rows, in, out_per, M, a.x_ld, mode);
+  if (!st) st = check_x(x, a.x_ld, a.xh);
   if (st) return st;
   if (bits < 4 || bits > 6 || (bits > 4 && !hb)) return RWKVQ_ERR_ARG;
   a.q = nib; a.hb = hb; a.rec = rec;
@@ -610,6 +727,7 @@ int rwkvq_gemm_sym(const uint8_t* codes, const uint32_t* hb, const int8_t* qs,
                    void* stream) {
   GemmArgs a = make_args(rows, in, out_per, x, x_ld, y, M, mode);
   int st = check_gemm(rows, in, out_per, M, a.x_ld, mode);
+  if (!st) st = check_x(x, a.x_ld, a.xh);
   if (st) return st;
   if ((bits != 6 && bits != 8) || (bits == 6 && !hb)) return RWKVQ_ERR_ARG;
   a.q = codes; a.hb = hb; a.qs = qs; a.d = d;
@@ -622,6 +740,7 @@ int rwkvq_gemm_rtn8(const int8_t* codes, const uint16_t* scale, int rows,
                     int M, int mode, void* stream) {
   GemmArgs a = make_args(rows, in, out_per, x, x_ld, y, M, mode);
   int st = check_gemm(rows, in, out_per, M, a.x_ld, mode);
+  if (!st) st = check_x(x, a.x_ld, a.xh);
   if (st) return st;
   a.q = reinterpret_cast<const uint8_t*>(codes); a.d = scale;
   return launch_gemm<F_RTN8>(a, (hipStream_t)stream);
@@ -630,14 +749,20 @@ int rwkvq_gemm_rtn8(const int8_t* codes, const uint16_t* scale, int rows,
 int rwkvq_gemm_f16(const uint16_t* w, int rows, int in, int out_per,
                    const float* x, long x_ld, float* y, int M, int mode,
                    int seg_modes, void* stream) {
+  const int flags = mode & ~15;
+  mode &= 15;
   GemmArgs a = make_args(rows, in, out_per, x, x_ld, y, M,
-                         mode == RWKVQ_EPI_PER_SEG ? 0 : mode);
-  int st = check_gemm(rows, in, out_per, M, a.x_ld, a.mode, kStepK);
+                         (mode == RWKVQ_EPI_PER_SEG ? 0 : mode) | flags);
+  int st = check_gemm(rows, in, out_per, M, a.x_ld,
+                      (mode == RWKVQ_EPI_PER_SEG ? 0 : mode) | flags, kStepK);
+  if (!st) st = check_x(x, a.x_ld, a.xh);
   if (st) return st;
   if (mode == RWKVQ_EPI_PER_SEG) {
     for (int j = 0; j < rows / out_per; ++j) {
       const int m = (seg_modes >> (4 * j)) & 15;
-      if (m > RWKVQ_EPI_SIGMOID || j >= 8) return RWKVQ_ERR_ARG;
+      if (m > RWKVQ_EPI_SIGMOID || j >= 8 ||
+          (a.yord >= 0 && m == RWKVQ_EPI_ADD))
+        return RWKVQ_ERR_ARG;
     }
     a.mode = mode;
     a.seg_modes = seg_modes;
@@ -648,23 +773,25 @@ int rwkvq_gemm_f16(const uint16_t* w, int rows, int in, int out_per,
 
 int rwkvq_gemm_f16_seg(const uint16_t* w, int nseg, const int* seg_rows,
                        int in, const float* x, long x_ld, float* y, int M,
-                       int seg_modes, void* stream) {
+                       int seg_modes, int flags, void* stream) {
   if (!w || !x || !y || nseg < 1 || nseg > 8 || in <= 0 || in % kStepK ||
-      M <= 0)
+      M <= 0 || (flags & 15) ||
+      check_gemm(128, 128, 128, 1, 128, flags, kStepK))
     return RWKVQ_ERR_ARG;
   int rows = 0;
-  GemmArgs a{};
-  a.split = 1;
+  GemmArgs a = make_args(128, 128, 128, x, x_ld, y, M, flags);
   for (int j = 0; j < nseg; ++j) {
     const int m = (seg_modes >> (4 * j)) & 15;
-    if (seg_rows[j] <= 0 || seg_rows[j] % 128 || m > RWKVQ_EPI_SIGMOID)
+    if (seg_rows[j] <= 0 || seg_rows[j] % 128 || m > RWKVQ_EPI_SIGMOID ||
+        (a.yord >= 0 && m == RWKVQ_EPI_ADD))
       return RWKVQ_ERR_ARG;
     rows += seg_rows[j];
     a.seg_end[j] = rows;
   }
   a.x = x; a.y = y; a.M = M; a.N = rows; a.in = in; a.out_per = rows;
   a.x_ld = x_ld > 0 ? x_ld : (long)nseg * in;
-  if (a.x_ld < (long)nseg * in) return RWKVQ_ERR_ARG;
+  if (a.x_ld < (long)nseg * in || check_x(x, a.x_ld, a.xh))
+    return RWKVQ_ERR_ARG;
   a.mode = RWKVQ_EPI_PER_SEG;
   a.seg_modes = seg_modes;
   a.nseg_tab = nseg;

@@ -127,16 +127,64 @@ __device__ __forceinline__ void row_stats4(const float4 (&v)[kMaxE4], int D,
   rstd = 1.f / sqrtf(var + eps);
 }
 
+// fp16 stores in a GEMM input pair order (within each 32-column group,
+// halves 2i, 2i+1 = columns (c0(i), c1(i)); RWKVQ_ORDER_*).  Lanes holding
+// consecutive columns form the groups, so a column's partner is held by the
+// lane at a fixed xor distance in the same wave; the lane of the lower
+// column writes the pair.  All lanes of a 32-column group must call these.
+//   store_pairs4: a lane holds columns c .. c + 3 (c % 4 == 0)
+// (the pins keep each value rounded to fp32 before its fp16 rounding, as
+// the fp32 output followed by a conversion: without them the compiler may
+// fuse the producing multiply-add and the conversion into one mixed-precision
+// instruction that rounds once)
+template <int ORD>
+__device__ __forceinline__ void store_pairs4(uint16_t* row, int c, float4 o) {
+  pin(o);
+  const uint32_t lo = pack_h2(o.x, o.y), hi = pack_h2(o.z, o.w);
+  if constexpr (ORD == RWKVQ_ORDER_PAIRS) {
+    *reinterpret_cast<uint2*>(row + c) = make_uint2(lo, hi);
+  } else {
+    constexpr int m = ORD == RWKVQ_ORDER_SB6 ? 4 : 2;   // partner c + 16 / 8
+    const uint32_t plo = __shfl_xor(lo, m, 64), phi = __shfl_xor(hi, m, 64);
+    const int cg = c & 31;
+    if (((cg >> 2) & m) == 0) {
+      const int pos = 2 * cg - (cg >= 16 ? 16 : 0);
+      *reinterpret_cast<uint4*>(row + (c - cg) + pos) =
+          make_uint4((lo & 0xFFFFu) | (plo << 16), (lo >> 16) | (plo & 0xFFFF0000u),
+                     (hi & 0xFFFFu) | (phi << 16), (hi >> 16) | (phi & 0xFFFF0000u));
+    }
+  }
+}
+//   store_pairs1: a lane holds column c
+template <int ORD>
+__device__ __forceinline__ void store_pairs1(uint16_t* row, int c, float v) {
+  pin(v);
+  constexpr int m = ORD == RWKVQ_ORDER_PAIRS ? 1
+                  : ORD == RWKVQ_ORDER_SB6 ? 16 : 8;
+  const uint32_t h = __builtin_bit_cast(uint16_t, (_Float16)v);
+  const uint32_t ph = __shfl_xor(h, m, 64);
+  const int cg = c & 31;
+  if ((cg & m) == 0) {
+    const int pos = ORD == RWKVQ_ORDER_PAIRS ? cg
+                                             : 2 * cg - (cg >= 16 ? 16 : 0);
+    *reinterpret_cast<uint32_t*>(row + (c - cg) + pos) = h | (ph << 16);
+  }
+}
+
 // LN + token shift + ncoef lerps for one token row (b, t):
 //   out[(b*T+t), k, :] = xn + (shift - xn) * coef[k, :]
 // shift = xn of (b, t-1), or prev[b] (zeros when prev is null) at t = 0.
 // new_prev[b] = xn of (b, T-1).
-template <int NC>
+// ORD < 0: fp32 out [N, NC, D]; ORD = RWKVQ_ORDER_*: fp16 out, each
+// 32-column group in that pair order (the input of the GEMM that reads it).
+template <int NC, int ORD>
 __global__ void __launch_bounds__(kRowThreads)
 shift_lerp_k(const float* __restrict__ x, const float* __restrict__ lw,
              const float* __restrict__ lb, const float* __restrict__ prev,
-             const float* __restrict__ coef, float* __restrict__ out,
+             const float* __restrict__ coef, void* __restrict__ out_,
              float* __restrict__ new_prev, int T, int D) {
+  float* out = static_cast<float*>(out_);
+  uint16_t* oh = static_cast<uint16_t*>(out_);
   __shared__ float sh[16];
   const int row = blockIdx.x;           // b * T + t
   const int t = row % T, bb = row / T;
@@ -181,7 +229,12 @@ shift_lerp_k(const float* __restrict__ x, const float* __restrict__ lw,
       o.y = xn[1] + xx[1] * cf[k][e].y;
       o.z = xn[2] + xx[2] * cf[k][e].z;
       o.w = xn[3] + xx[3] * cf[k][e].w;
-      *reinterpret_cast<float4*>(out + ((size_t)row * NC + k) * D + c) = o;
+      const size_t base = ((size_t)row * NC + k) * D;
+      if constexpr (ORD < 0) {
+        *reinterpret_cast<float4*>(out + base + c) = o;
+      } else {
+        store_pairs4<ORD>(oh + base, c, o);
+      }
     }
     if (t == T - 1 && new_prev)
       *reinterpret_cast<float4*>(new_prev + (size_t)bb * D + c) =
@@ -364,12 +417,13 @@ wkv_scan_k(const float* __restrict__ r, long r_ld,
 }
 
 // Group norm per head + bonus + gate.  One wave = one (token, head).
+template <int ORD>   // < 0: fp32 out; else fp16 in pair order ORD
 __global__ void __launch_bounds__(256)
 wkv_tail_k(const float* __restrict__ y, const float* __restrict__ rkv,
            const float* __restrict__ kp, const float* __restrict__ vp,
            const float* __restrict__ g, const float* __restrict__ r_k,
            const float* __restrict__ lnw, const float* __restrict__ lnb,
-           float* __restrict__ out, int D) {
+           void* __restrict__ out, int D) {
   const int n = blockIdx.y;
   const int c = blockIdx.x * blockDim.x + threadIdx.x;
   const size_t e = (size_t)n * D + c;
@@ -380,7 +434,11 @@ wkv_tail_k(const float* __restrict__ y, const float* __restrict__ rkv,
   const float nrm = dv / sqrtf(var + 64e-5f);
   const float r = rkv[(size_t)n * 3 * D + c];
   const float dp = wave_sum_dpp(r * kp[e] * r_k[c]);
-  out[e] = ((nrm * lnw[c] + lnb[c]) + dp * vp[e]) * g[e];
+  const float o = ((nrm * lnw[c] + lnb[c]) + dp * vp[e]) * g[e];
+  if constexpr (ORD < 0)
+    static_cast<float*>(out)[e] = o;
+  else
+    store_pairs1<ORD>(static_cast<uint16_t*>(out) + (size_t)n * D, c, o);
 }
 
 // Decode (T = 1) time-mix core for one (sequence, head) per block: the
@@ -946,6 +1004,29 @@ inline int ok_launch() {
 
 }  // namespace
 
+namespace {
+
+template <int NC>
+void launch_lerp_f16(int order, int rows, hipStream_t s, const float* x,
+                     const float* lw, const float* lb, const float* prev,
+                     const float* coef, uint16_t* out, float* new_prev, int T,
+                     int D) {
+  if (order == RWKVQ_ORDER_PAIRS)
+    hipLaunchKernelGGL((shift_lerp_k<NC, RWKVQ_ORDER_PAIRS>), dim3(rows),
+                       dim3(kRowThreads), 0, s, x, lw, lb, prev, coef, out,
+                       new_prev, T, D);
+  else if (order == RWKVQ_ORDER_SB6)
+    hipLaunchKernelGGL((shift_lerp_k<NC, RWKVQ_ORDER_SB6>), dim3(rows),
+                       dim3(kRowThreads), 0, s, x, lw, lb, prev, coef, out,
+                       new_prev, T, D);
+  else
+    hipLaunchKernelGGL((shift_lerp_k<NC, RWKVQ_ORDER_SYM6>), dim3(rows),
+                       dim3(kRowThreads), 0, s, x, lw, lb, prev, coef, out,
+                       new_prev, T, D);
+}
+
+}  // namespace
+
 extern "C" {
 
 int rwkvq_layer_norm(const float* x, const float* w, const float* b, float* y,
@@ -964,12 +1045,30 @@ int rwkvq_shift_lerp(const float* x, const float* ln_w, const float* ln_b,
       D % 4 || (ncoef != 1 && ncoef != 6))
     return RWKVQ_ERR_ARG;
   if (ncoef == 6)
-    hipLaunchKernelGGL(shift_lerp_k<6>, dim3(B * T), dim3(kRowThreads), 0,
-                       (hipStream_t)stream, x, ln_w, ln_b, prev, coef, out,
+    hipLaunchKernelGGL((shift_lerp_k<6, -1>), dim3(B * T), dim3(kRowThreads),
+                       0, (hipStream_t)stream, x, ln_w, ln_b, prev, coef, out,
                        new_prev, T, D);
   else
-    hipLaunchKernelGGL(shift_lerp_k<1>, dim3(B * T), dim3(kRowThreads), 0,
-                       (hipStream_t)stream, x, ln_w, ln_b, prev, coef, out,
+    hipLaunchKernelGGL((shift_lerp_k<1, -1>), dim3(B * T), dim3(kRowThreads),
+                       0, (hipStream_t)stream, x, ln_w, ln_b, prev, coef, out,
+                       new_prev, T, D);
+  return ok_launch();
+}
+
+int rwkvq_shift_lerp_f16(const float* x, const float* ln_w, const float* ln_b,
+                         const float* prev, const float* coef, int ncoef,
+                         uint16_t* out, int order, float* new_prev, int B,
+                         int T, int D, void* stream) {
+  if (B <= 0 || T <= 0 || D <= 0 || D > 4 * kRowThreads * kMaxE4 ||
+      D % 32 || (ncoef != 1 && ncoef != 6) || order < 0 ||
+      order > RWKVQ_ORDER_SYM6 || reinterpret_cast<uintptr_t>(out) % 16)
+    return RWKVQ_ERR_ARG;
+  hipStream_t s = (hipStream_t)stream;
+  if (ncoef == 6)
+    launch_lerp_f16<6>(order, B * T, s, x, ln_w, ln_b, prev, coef, out,
+                       new_prev, T, D);
+  else
+    launch_lerp_f16<1>(order, B * T, s, x, ln_w, ln_b, prev, coef, out,
                        new_prev, T, D);
   return ok_launch();
 }
@@ -1033,9 +1132,30 @@ int rwkvq_wkv_tail(const float* y, const float* rkv, const float* kp,
                    const float* ln_w, const float* ln_b, float* out, int N,
                    int D, int head_size, void* stream) {
   if (N <= 0 || D % 256 || head_size != kHead) return RWKVQ_ERR_ARG;
-  hipLaunchKernelGGL(wkv_tail_k, dim3(D / 256, N), dim3(256), 0,
+  hipLaunchKernelGGL(wkv_tail_k<-1>, dim3(D / 256, N), dim3(256), 0,
                      (hipStream_t)stream, y, rkv, kp, vp, g, r_k, ln_w, ln_b,
                      out, D);
+  return ok_launch();
+}
+
+int rwkvq_wkv_tail_f16(const float* y, const float* rkv, const float* kp,
+                       const float* vp, const float* g, const float* r_k,
+                       const float* ln_w, const float* ln_b, uint16_t* out,
+                       int order, int N, int D, int head_size, void* stream) {
+  if (N <= 0 || D % 256 || head_size != kHead || order < 0 ||
+      order > RWKVQ_ORDER_SYM6 || reinterpret_cast<uintptr_t>(out) % 4)
+    return RWKVQ_ERR_ARG;
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid(D / 256, N);
+  if (order == RWKVQ_ORDER_PAIRS)
+    hipLaunchKernelGGL(wkv_tail_k<RWKVQ_ORDER_PAIRS>, grid, dim3(256), 0, s,
+                       y, rkv, kp, vp, g, r_k, ln_w, ln_b, out, D);
+  else if (order == RWKVQ_ORDER_SB6)
+    hipLaunchKernelGGL(wkv_tail_k<RWKVQ_ORDER_SB6>, grid, dim3(256), 0, s, y,
+                       rkv, kp, vp, g, r_k, ln_w, ln_b, out, D);
+  else
+    hipLaunchKernelGGL(wkv_tail_k<RWKVQ_ORDER_SYM6>, grid, dim3(256), 0, s,
+                       y, rkv, kp, vp, g, r_k, ln_w, ln_b, out, D);
   return ok_launch();
 }
 

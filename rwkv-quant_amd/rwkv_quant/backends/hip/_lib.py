@@ -17,6 +17,10 @@ ERRORS = {1001: "invalid argument or shape", 1002: "kernel launch failed",
 
 EPI_STORE, EPI_ADD, EPI_RELU2, EPI_TANH, EPI_SIGMOID = 0, 1, 2, 3, 4
 EPI_PER_SEG = 5                # rwkvq_gemm_f16: mode per input segment
+X_F16 = 16                     # GEMM flag: x is fp16 in the format's pair order
+Y_F16 = 32                     # GEMM flag: y is fp16 in pair order (bits 6-7)
+Y_ORDER_SHIFT = 6
+ORDER_PAIRS, ORDER_SB6, ORDER_SYM6 = 0, 1, 2
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -35,8 +39,9 @@ SIGNATURES = {
     "rwkvq_gemm_rtn8": [_P, _P, _I, _I, _I, _P, _L, _P, _I, _I, _P],
     "rwkvq_gemm_f16": [_P, _I, _I, _I, _P, _L, _P, _I, _I, _I, _P],
     "rwkvq_gemv_f16_seg": [_P, _I, _P, _I, _P, _L, _P, _I, _I, _P],
-    "rwkvq_gemm_f16_seg": [_P, _I, _P, _I, _P, _L, _P, _I, _I, _P],
+    "rwkvq_gemm_f16_seg": [_P, _I, _P, _I, _P, _L, _P, _I, _I, _I, _P],
     "rwkvq_gemm_workspace": [_P, _L, _P, _I],
+    "rwkvq_x16": [_P, _L, _I, _I, _I, _P, _L, _P],
     "rwkvq_dequant_sb6_f32": [_P, _P, _P, _I, _I, _I, _P, _I, _P],
     "rwkvq_dequant_sym_f32": [_P, _P, _P, _P, _I, _I, _I, _P, _I, _P],
     "rwkvq_dequant_rtn8_f32": [_P, _P, _I, _I, _P, _I, _P],
@@ -47,6 +52,8 @@ SIGNATURES = {
                               _P],
     "rwkvq_layer_norm": [_P, _P, _P, _P, _I, _I, _F, _P],
     "rwkvq_shift_lerp": [_P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _P],
+    "rwkvq_shift_lerp_f16": [_P, _P, _P, _P, _P, _I, _P, _I, _P, _I, _I, _I,
+                             _P],
     "rwkvq_wkv_prep": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P,
                        _P, _P, _P, _I, _I, _I, _P],
     "rwkvq_wkv7_scan": [_P, _L, _P, _P, _P, _P, _P, _L, _P, _P, _P, _L, _I,
@@ -54,6 +61,8 @@ SIGNATURES = {
     "rwkvq_wkv7_scan_chunked": [_P, _L, _P, _P, _P, _P, _P, _L, _P, _P, _P,
                                 _L, _I, _I, _I, _I, _P, _L, _P],
     "rwkvq_wkv_tail": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P],
+    "rwkvq_wkv_tail_f16": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I,
+                           _I, _P],
     "rwkvq_lora_gemv": [_I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P],
     "rwkvq_wkv7_decode_lora": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                _P, _P, _I, _P, _P, _P, _I, _I, _I, _P],
@@ -114,6 +123,10 @@ def ensure_gemm_workspace():
 
 def call(name, *args):
     """Invoke an entry point; a non-zero status raises HipKernelError."""
+    if len(args) != len(SIGNATURES[name]):
+        # ctypes would pass extra arguments on (as to a varargs function)
+        raise TypeError(f"{name}: {len(args)} arguments, the C entry point "
+                        f"takes {len(SIGNATURES[name])}")
     if name.startswith("rwkvq_gemm_") and name != "rwkvq_gemm_workspace":
         ensure_gemm_workspace()
     st = getattr(load(), name)(*args)

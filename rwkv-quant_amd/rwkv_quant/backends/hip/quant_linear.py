@@ -150,6 +150,9 @@ class _HipLinearBase:
     def _f16_args(self):
         return None
 
+    # pair order of the fp16 GEMM input (RWKVQ_X_F16); None: fp32 only
+    x16_order = None
+
 
 class GwQuantLinear(_HipLinearBase):
     """sb6 tensor (gs 32, sb 8, bits 4/5/6)."""
@@ -176,6 +179,8 @@ class GwQuantLinear(_HipLinearBase):
     def _kargs(self):
         return "sb6", (_lib.ptr(self.nib), _lib.ptr(self.hb),
                        _lib.ptr(self.rec), self.bits)
+
+    x16_order = _lib.ORDER_SB6
 
     def _f16_args(self):
         return (self.bits - 4, self.nib, self.hb, self.rec, None, None)
@@ -233,6 +238,10 @@ class SymQuantLinear(_HipLinearBase):
         return "sym", (_lib.ptr(self.codes), _lib.ptr(self.hb),
                        _lib.ptr(self.qs), _lib.ptr(self.d), self.bits)
 
+    @property
+    def x16_order(self):
+        return _lib.ORDER_SYM6 if self.bits == 6 else _lib.ORDER_PAIRS
+
     def _f16_args(self):
         return (3 if self.bits == 6 else 4, self.codes, self.hb, None,
                 self.qs, self.d)
@@ -269,6 +278,11 @@ class QuantLinearV2(_HipLinearBase):
 
     def _kargs(self):
         return "rtn8", (_lib.ptr(self.codes), _lib.ptr(self.scale))
+
+    @property
+    def x16_order(self):
+        # the outlier correction reads x in fp32
+        return None if self.has_outliers else _lib.ORDER_PAIRS
 
     def _run(self, kind, x2, y, out_per=None, mode=_lib.EPI_STORE, n=None,
              x_ld=0):
@@ -307,6 +321,10 @@ class _FusedBase:
         self.out_per = l0.out_features
         self.out_features = self.out_per * self.K
         self.in_features = l0.in_features
+
+    @property
+    def x16_order(self):
+        return self._cat.x16_order
 
     def gemv_into(self, x, y, n, x_ld, mode=_lib.EPI_STORE):
         """y [n, K * out_per] <- the K matrices applied to their own inputs:

@@ -51,6 +51,8 @@ WKV_CHUNK_MIN_T = 32           # sequence length from which the WKV scan
                                # runs in 16-step chunks (operators + a
                                # sequential pass on the matrix cores)
 WKV_CHUNK_OPS = 6400           # operator floats per (sequence, head, chunk)
+X16_PREFILL = True             # prefill GEMM inputs written as fp16 in the
+                               # GEMM's pair order by their producers
 
 _LORA = ("w1", "w2", "a1", "a2", "v1", "v2", "g1", "g2")
 
@@ -158,6 +160,14 @@ class _Work:
         self.xk = torch.empty(N, C, **f)
         self.hk = torch.empty(N, ffn, **f)
         self.xo = torch.empty(N, C, **f)
+        if N >= GEMM_MIN_BATCH_NB:
+            # prefill GEMM inputs as fp16, each in its GEMM's pair order
+            h = dict(dtype=torch.float16, device=device)
+            self.xs16 = torch.empty(N, 6, C, **h)
+            self.o16 = torch.empty(N, C, **h)
+            self.xk16 = torch.empty(N, C, **h)
+            self.hk16 = torch.empty(N, ffn, **h)
+            self.h16 = torch.empty(N, rp, **h)
 
 
 class QuantTMix:
@@ -246,7 +256,9 @@ class QuantTMix:
     EPI_DOWN = {"w": _lib.EPI_TANH, "a": _lib.EPI_STORE, "v": _lib.EPI_STORE,
                 "g": _lib.EPI_SIGMOID}
 
-    def run_lora(self, wk):
+    def run_lora(self, wk, x16_order=None):
+        """x16_order (prefill): the lerp outputs are the fp16 wk.xs16 in
+        that pair order; the down outputs go to wk.h16 as fp16."""
         N, C = wk.N, self.C
         branches = list(self.lora)
         if N <= LORA_KERNEL_MAX_N:
@@ -260,30 +272,51 @@ class QuantTMix:
         # prefill: the MFMA GEMM over the dense fp16 factors; one launch for
         # the down products of all branches (their lerp slots v, w, a, g are
         # adjacent in wk.xs), one per up product
-        order, rps, A_cat, B_pad, modes = self._prefill_mats()
-        xs_flat = wk.xs.view(N, 6 * C)
+        x16 = x16_order is not None
+        order, rps, A_cat, B_pad, modes = self._prefill_mats(
+            x16_order if x16 else _lib.ORDER_PAIRS)
+        xs_flat = (wk.xs16 if x16 else wk.xs).view(N, 6 * C)
+        hbuf = wk.h16 if x16 else wk.h_cat
         s0 = self.SLOT[order[0]]
         nseg, tot = len(order), sum(rps)
+        flags = (_lib.X_F16 | _lib.Y_F16
+                 | (_lib.ORDER_PAIRS << _lib.Y_ORDER_SHIFT)) if x16 else 0
         _lib.call("rwkvq_gemm_f16_seg", _lib.ptr(A_cat), nseg,
                   (ctypes.c_int * nseg)(*rps), C,
-                  _lib.ptr(xs_flat[:, s0 * C:]), 6 * C, _lib.ptr(wk.h_cat), N,
-                  modes, _stream())
+                  _lib.ptr(xs_flat[:, s0 * C:]), 6 * C, _lib.ptr(hbuf), N,
+                  modes, flags, _stream())
         # the down GEMM wrote rows of `tot` values, branch j from column
         # sum(rps[:j]) on
-        hc = wk.h_cat.view(-1)[:N * tot].view(N, tot)
+        hc = hbuf.view(-1)[:N * tot].view(N, tot)
         off = 0
         for j, b in enumerate(order):
             _lib.call("rwkvq_gemm_f16", _lib.ptr(B_pad[b]), C, rps[j], C,
                       _lib.ptr(hc[:, off:]), tot, _lib.ptr(wk.yl[b]), N,
-                      _lib.EPI_STORE, 0, _stream())
+                      _lib.EPI_STORE | (_lib.X_F16 if x16 else 0), 0,
+                      _stream())
             off += rps[j]
 
-    def _prefill_mats(self):
+    def _prefill_mats(self, x_order=_lib.ORDER_PAIRS):
         """Prefill LoRA factors padded for the GEMM tiles (built on first
         use): down factors stacked in lerp-slot order (v, w, a, g), each
-        padded with zero rows to a multiple of 128 (rps); up factors padded
-        with zero columns to the same width.  Padded outputs multiply zero
-        weights."""
+        padded with zero rows to a multiple of 128 (rps), their columns in
+        pair order x_order (that of the fp16 lerp outputs they read: the
+        GEMM pairs halves 2i, 2i+1, so permuting W's columns like x's keeps
+        the product); up factors padded with zero columns to the same
+        width.  Padded outputs multiply zero weights."""
+        cache = self.__dict__.setdefault("_pmats_by_order", {})
+        if x_order not in cache:
+            order, rps, A_cat, B_pad, modes = self._prefill_mats_base()
+            if x_order != _lib.ORDER_PAIRS:
+                C = self.C
+                idx = torch.as_tensor(pair_cols(x_order), device=A_cat.device)
+                idx = (torch.arange(0, C, 32, device=A_cat.device)[:, None]
+                       + idx[None]).reshape(-1)
+                A_cat = A_cat[:, idx].contiguous()
+            cache[x_order] = (order, rps, A_cat, B_pad, modes)
+        return cache[x_order]
+
+    def _prefill_mats_base(self):
         if getattr(self, "_pmats", None) is None:
             order = [b for b in ("v", "w", "a", "g") if b in self.lora]
             C = self.C
@@ -387,6 +420,37 @@ class QuantBlock:
         self.cmix = QuantCMix(tensors, prefix, naming, device)
 
 
+def pair_cols(order):
+    """Source column of each fp16 position of a 32-column group in pair
+    order `order` (RWKVQ_ORDER_*): halves 2i, 2i+1 hold (c0(i), c1(i))."""
+    cols = []
+    for i in range(16):
+        if order == _lib.ORDER_SB6:
+            cols += [i, i + 16]
+        elif order == _lib.ORDER_SYM6:
+            c0 = i if i < 8 else i + 8
+            cols += [c0, c0 + 8]
+        else:
+            cols += [2 * i, 2 * i + 1]
+    return cols
+
+
+def _x16_orders(blk):
+    """Pair orders of the fp16 inputs of the block's prefill GEMMs (r/k/v,
+    output, channel-mix key, value), or None where a matrix has no fp16
+    input path (dense fallback, rtn outliers, shapes off the MFMA tiles)."""
+    tm, cm = blk.tmix, blk.cmix
+    rf = tm.rkv_fused
+    if not FUSE or rf is None or not rf._cat.gemm_ok(rf.out_per):
+        return None
+    lins = (rf, tm.o_proj, cm.key, cm.value)
+    orders = [getattr(l, "x16_order", None) for l in lins]
+    if any(o is None for o in orders) or not all(
+            l.gemm_ok() for l in lins[1:]):
+        return None
+    return orders
+
+
 def _apply(lin, x2, y, mode, n=None, x_ld=0):
     """y <- epi(x2 @ W^T): GEMV kernel for small N, MFMA GEMM for prefill
     (both with the epilogue fused)."""
@@ -476,11 +540,19 @@ class QuantRWKV7:
         self.emb.gather_into(idx.reshape(-1), x)
         _lib.call("rwkvq_layer_norm", _lib.ptr(x), _lib.ptr(self.ln0_w),
                   _lib.ptr(self.ln0_b), _lib.ptr(x), N, C, 1e-5, st)
+        x16 = (X16_PREFILL and T > 1 and N >= GEMM_MIN_BATCH_NB
+               and N > LORA_KERNEL_MAX_N)
         for li, (blk, state) in enumerate(zip(self.blocks, states)):
             tm, cm = blk.tmix, blk.cmix
             wkv_in, tshift, cshift = state
             wkv_out, tshift_out, cshift_out = out_states[li]
             layer0 = 1 if li == 0 else 0
+            orders = _x16_orders(blk) if x16 else None
+            if orders is not None:
+                self._layer_x16(blk, orders, x, tshift, cshift, wkv_in,
+                                wkv_out, tshift_out, cshift_out, layer0, wk,
+                                B, T)
+                continue
             _lib.call("rwkvq_shift_lerp", _lib.ptr(x), _lib.ptr(blk.ln1_w),
                       _lib.ptr(blk.ln1_b), _lib.ptr(tshift),
                       _lib.ptr(tm.coef), 6, _lib.ptr(wk.xs),
@@ -529,7 +601,32 @@ class QuantRWKV7:
         _lib.call("rwkvq_layer_norm", _lib.ptr(x), _lib.ptr(self.ln_out_w),
                   _lib.ptr(self.ln_out_b), _lib.ptr(wk.xo), N, C, 1e-5, st)
 
-    def _wkv_seq(self, tm, wk, wkv_in, wkv_out, layer0, B, T, st):
+    def _layer_x16(self, blk, orders, x, tshift, cshift, wkv_in, wkv_out,
+                   tshift_out, cshift_out, layer0, wk, B, T):
+        """One prefill layer with every GEMM input fp16, written by its
+        producer in the GEMM's pair order: the lerp kernel (r/k/v + LoRA
+        down, channel-mix key), the time-mix tail (output projection), the
+        key GEMM's epilogue (value)."""
+        tm, cm = blk.tmix, blk.cmix
+        N, C = B * T, self.n_embd
+        st = _stream()
+        o_r, o_o, o_k, o_v = orders
+        _lib.call("rwkvq_shift_lerp_f16", _lib.ptr(x), _lib.ptr(blk.ln1_w),
+                  _lib.ptr(blk.ln1_b), _lib.ptr(tshift), _lib.ptr(tm.coef), 6,
+                  _lib.ptr(wk.xs16), o_r, _lib.ptr(tshift_out), B, T, C, st)
+        tm.rkv_fused.apply_into(wk.xs16, wk.rkv, N, 6 * C, mode=_lib.X_F16)
+        tm.run_lora(wk, x16_order=o_r)
+        self._wkv_seq(tm, wk, wkv_in, wkv_out, layer0, B, T, st, o16=o_o)
+        tm.o_proj.apply_into(wk.o16, x, mode=_lib.EPI_ADD | _lib.X_F16, n=N)
+        _lib.call("rwkvq_shift_lerp_f16", _lib.ptr(x), _lib.ptr(blk.ln2_w),
+                  _lib.ptr(blk.ln2_b), _lib.ptr(cshift), _lib.ptr(cm.x_k), 1,
+                  _lib.ptr(wk.xk16), o_k, _lib.ptr(cshift_out), B, T, C, st)
+        cm.key.apply_into(wk.xk16, wk.hk16, n=N,
+                          mode=(_lib.EPI_RELU2 | _lib.X_F16 | _lib.Y_F16
+                                | (o_v << _lib.Y_ORDER_SHIFT)))
+        cm.value.apply_into(wk.hk16, x, mode=_lib.EPI_ADD | _lib.X_F16, n=N)
+
+    def _wkv_seq(self, tm, wk, wkv_in, wkv_out, layer0, B, T, st, o16=None):
         """T > 1: per-channel inputs, the scan (step by step, or from
         WKV_CHUNK_MIN_T on in 16-step chunks), tail."""
         N, C, H = B * T, self.n_embd, self.n_head
@@ -558,6 +655,13 @@ class QuantRWKV7:
                       _lib.ptr(wk.aa), _lib.ptr(wk.bb), C, _lib.ptr(wkv_in),
                       _lib.ptr(wkv_out), _lib.ptr(wk.y), C, B, T, H,
                       self.head_size, st)
+        if o16 is not None:                 # fp16 in the o GEMM's order
+            _lib.call("rwkvq_wkv_tail_f16", _lib.ptr(wk.y), _lib.ptr(wk.rkv),
+                      _lib.ptr(wk.kp), _lib.ptr(wk.vp), _lib.ptr(wk.yl["g"]),
+                      _lib.ptr(tm.r_k), _lib.ptr(tm.ln_x_w),
+                      _lib.ptr(tm.ln_x_b), _lib.ptr(wk.o16), o16, N, C,
+                      self.head_size, st)
+            return
         _lib.call("rwkvq_wkv_tail", _lib.ptr(wk.y), _lib.ptr(wk.rkv),
                   _lib.ptr(wk.kp), _lib.ptr(wk.vp), _lib.ptr(wk.yl["g"]),
                   _lib.ptr(tm.r_k), _lib.ptr(tm.ln_x_w), _lib.ptr(tm.ln_x_b),

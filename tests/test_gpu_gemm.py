@@ -224,7 +224,7 @@ def test_gemm_f16_segment_table(M):
     sm = sum(m << (4 * j) for j, m in enumerate(modes))
     _lib.call("rwkvq_gemm_f16_seg", _lib.ptr(Ad), 4,
               (ctypes.c_int * 4)(*rows), K, _lib.ptr(xd[:, 2]), 6 * K,
-              _lib.ptr(y), M, sm, _lib.stream_handle())
+              _lib.ptr(y), M, sm, 0, _lib.stream_handle())
     fns = {_lib.EPI_STORE: lambda v: v, _lib.EPI_TANH: np.tanh,
            _lib.EPI_SIGMOID: lambda v: 1 / (1 + np.exp(-v))}
     off = 0
@@ -242,7 +242,7 @@ def test_gemm_f16_segment_table(M):
     with pytest.raises(_lib.HipKernelError):      # a segment off the tiles
         _lib.call("rwkvq_gemm_f16_seg", _lib.ptr(Ad), 2,
                   (ctypes.c_int * 2)(100, 668), K, _lib.ptr(xd[:, 2]),
-                  6 * K, _lib.ptr(y), M, 0, _lib.stream_handle())
+                  6 * K, _lib.ptr(y), M, 0, 0, _lib.stream_handle())
 
 
 def _set_split(on):
@@ -278,3 +278,56 @@ def test_gemm_split_k(kind, bits, shape, mode):
     assert torch.allclose(outs[0], ref, rtol=1e-5, atol=1e-5)
     _, cnt = _lib._gemm_ws[torch.cuda.current_device()]
     assert int(cnt.abs().sum()) == 0             # counters re-armed
+
+
+def _pair_cols(order):
+    """Source column of each fp16 position within a 32-column group."""
+    c = []
+    for i in range(16):
+        if order == _lib.ORDER_SB6:
+            c += [i, i + 16]
+        elif order == _lib.ORDER_SYM6:
+            c0 = i if i < 8 else i + 8
+            c += [c0, c0 + 8]
+        else:
+            c += [2 * i, 2 * i + 1]
+    return np.array(c)
+
+
+def _order_of(kind, bits):
+    if kind == "sb6":
+        return _lib.ORDER_SB6
+    return _lib.ORDER_SYM6 if (kind, bits) == ("sym", 6) else _lib.ORDER_PAIRS
+
+
+def _to_x16(x, order, cols=None):
+    M, C = x.shape[0], cols or x.shape[1]
+    xh = torch.empty(M, C, dtype=torch.float16, device="cuda")
+    _lib.call("rwkvq_x16", _lib.ptr(x), x.stride(0), C, M, order,
+              _lib.ptr(xh), C, _lib.stream_handle())
+    return xh
+
+
+@pytest.mark.parametrize("order", [0, 1, 2])
+def test_x16_pair_order(order):
+    """fp32 -> fp16 (nearest even) with each 32-column group permuted into
+    the pair order of the formats' decoders."""
+    x = act(5, 256, seed=order).cuda()
+    xh = _to_x16(x, order).cpu().numpy().reshape(5, 8, 32)
+    src = x.half().cpu().numpy().reshape(5, 8, 32)
+    assert np.array_equal(xh, src[:, :, _pair_cols(order)])
+
+
+@pytest.mark.parametrize("kind,bits", FORMATS)
+@pytest.mark.parametrize("M", [37, 512])
+def test_gemm_x16_input_equals_fp32_input(kind, bits, M):
+    """The GEMM fed fp16 x in the format's pair order (RWKVQ_X_F16) gives the
+    bits of the same GEMM fed fp32 x (which rounds x to fp16 itself)."""
+    print(f"x16 gemm {kind}@{bits} M={M}", flush=True)
+    lin = LIN[kind](qt_for(kind, bits, _w(2048, 2048, seed=11)))
+    x = act(M, 2048, seed=12).cuda()
+    ref = _gemm(lin, x)
+    xh = _to_x16(x, _order_of(kind, bits))
+    y = torch.empty_like(ref)
+    lin._run("gemm", xh, y, mode=_lib.X_F16, n=M)
+    assert torch.equal(y, ref)
