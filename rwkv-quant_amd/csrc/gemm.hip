@@ -280,29 +280,42 @@ gemm_kernel(GemmArgs a) {
     // itself the scheduler sinks them next to their use
     __builtin_amdgcn_sched_barrier(0);
     const _Float16* xs = sx[kg][i & 1];
+    // The step's 8 MFMA rounds k = (group gi, 16-column sub-step ss) are
+    // software-pipelined: the x fragments of round k + 1 are read from LDS
+    // while round k's MFMAs run, and group 1's weights are decoded during
+    // group 0's rounds, so no MFMA waits on a just-issued LDS read.
+    auto read_bx = [&](int k, half8_t (&b)[WM]) {
+      const int gi = k >> 2, ss = k & 3;
 #pragma unroll
-    for (int gi = 0; gi < 2; ++gi) {
-      uint32_t w[WN][16];
-      const int kb = (c * 4 + 2 * h + gi) & 7;   // group within superblock
+      for (int mi = 0; mi < WM; ++mi)
+        b[mi] = *reinterpret_cast<const half8_t*>(
+            xs + (mi * 32 + r) * kRowH + (2 * h + gi) * 32 + ss * 8);
+    };
+    uint32_t w[2][WN][16];
+    half8_t bx[2][WM];
+    read_bx(0, bx[0]);
 #pragma unroll
-      for (int ni = 0; ni < WN; ++ni) weights_of<FMT>(cur[ni], gi, kb, w[ni]);
+    for (int ni = 0; ni < WN; ++ni)
+      weights_of<FMT>(cur[ni], 0, (c * 4 + 2 * h) & 7, w[0][ni]);
 #pragma unroll
-      for (int ss = 0; ss < 4; ++ss) {
-        half8_t bx[WM];
+    for (int k = 0; k < 8; ++k) {
+      const int gi = k >> 2, ss = k & 3;
+      if (k + 1 < 8) read_bx(k + 1, bx[(k + 1) & 1]);
+      if (k == 1) {
+#pragma unroll
+        for (int ni = 0; ni < WN; ++ni)
+          weights_of<FMT>(cur[ni], 1, (c * 4 + 2 * h + 1) & 7, w[1][ni]);
+      }
+#pragma unroll
+      for (int ni = 0; ni < WN; ++ni) {
+        const uint4 wa = make_uint4(w[gi][ni][4 * ss], w[gi][ni][4 * ss + 1],
+                                    w[gi][ni][4 * ss + 2],
+                                    w[gi][ni][4 * ss + 3]);
+        const half8_t av = __builtin_bit_cast(half8_t, wa);
 #pragma unroll
         for (int mi = 0; mi < WM; ++mi)
-          bx[mi] = *reinterpret_cast<const half8_t*>(
-              xs + (mi * 32 + r) * kRowH + (2 * h + gi) * 32 + ss * 8);
-#pragma unroll
-        for (int ni = 0; ni < WN; ++ni) {
-          const uint4 wa = make_uint4(w[ni][4 * ss], w[ni][4 * ss + 1],
-                                      w[ni][4 * ss + 2], w[ni][4 * ss + 3]);
-          const half8_t av = __builtin_bit_cast(half8_t, wa);
-#pragma unroll
-          for (int mi = 0; mi < WM; ++mi)
-            acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                av, bx[mi], acc[mi][ni], 0, 0, 0);
-        }
+          acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+              av, bx[k & 1][mi], acc[mi][ni], 0, 0, 0);
       }
     }
     // the prefetched registers are consumed only from here on
@@ -529,6 +542,7 @@ gemm_kernel(GemmArgs a) {
 #define RWKVQ_SPLIT_WGS 192
 #endif
 constexpr int kMinRun = 8;
+constexpr int kLongRun = 32;
 
 // Split-K workspace registered by the caller (rwkvq_gemm_workspace), one
 // per device.
@@ -550,7 +564,7 @@ const SplitWs* current_ws() {
 // SIMD (all tiles but 256 x 128) and the step count is even.
 template <int FMT, int WN, int WM>
 int launch_tile(const GemmArgs& a, hipStream_t s, int split = 1,
-                const SplitWs* ws = nullptr) {
+                const SplitWs* ws = nullptr, bool one_group = false) {
   GemmArgs b = a;
   b.nt = a.N / (128 * WN);
   b.mt = (a.M + 32 * WM - 1) / (32 * WM);
@@ -559,7 +573,7 @@ int launch_tile(const GemmArgs& a, hipStream_t s, int split = 1,
   const int grid = b.nt * b.mt * split;
   constexpr bool two = RWKVQ_GEMM_KG == 2 && WN * WM <= 4;
   constexpr int KG2 = two ? 2 : 1;
-  if (two && (a.in / kStepK / split) % 2 == 0) {
+  if (two && !one_group && (a.in / kStepK / split) % 2 == 0) {
     if (a.xh)
       hipLaunchKernelGGL((gemm_kernel<FMT, WN, WM, KG2, true>), dim3(grid),
                          dim3(512), 0, s, b);
@@ -591,9 +605,25 @@ int launch_gemm(const GemmArgs& a, hipStream_t s) {
   const int nsteps = a.in / kStepK;
   const bool wide = a.out_per % 256 == 0 && a.nseg_tab == 0;
   if (wide && wgs(256, 128) >= 256) return launch_tile<FMT, 2, 4>(a, s);
+  const SplitWs* ws = current_ws();
+  if (RWKVQ_GEMM_SPLIT && a.M > 64) {
+    // Two 4-wave workgroups per CU (each with its own barrier, so the two
+    // waves of a SIMD drift out of phase and overlap decode with MFMA)
+    // where the launch has >= 512 of them, splitting K only into runs of
+    // >= kLongRun steps (the partial tiles cost more than they save on
+    // shorter runs).
+    const long t = wgs(128, 128);
+    int split = 1;
+    while (t * split < 512 && split < 8 && nsteps % (2 * split) == 0 &&
+           nsteps / (2 * split) >= kLongRun && ws && t <= ws->ncnt &&
+           t * 2 * split * 128 * 128 * (long)sizeof(float) <= ws->bytes)
+      split *= 2;
+    if (t * split >= 512)
+      return launch_tile<FMT, 1, 4>(a, s, split, split > 1 ? ws : nullptr,
+                                    true);
+  }
   if (RWKVQ_GEMM_SPLIT && a.M > 64 && nsteps % 2 == 0) {
     const long t = wgs(128, 128);
-    const SplitWs* ws = current_ws();
     int split = 1;
     while (t * split < RWKVQ_SPLIT_WGS && split < 8 &&
            nsteps % (2 * kMinRun * split) == 0 && ws && t <= ws->ncnt &&
