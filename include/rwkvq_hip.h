@@ -60,6 +60,9 @@ extern "C" {
 #define RWKVQ_X_F16 16
 #define RWKVQ_Y_F16 32
 #define RWKVQ_Y_ORDER_SHIFT 6
+/* GEMM flag: do not split K (the split-K workspace serves one stream; a
+ * GEMM launched concurrently on another stream passes this) */
+#define RWKVQ_NO_SPLIT 256
 /* Pair orders of fp16 GEMM inputs: within each 32-column group, halves
  * 2i, 2i+1 hold columns (c0(i), c1(i)) -- the order in which the format's
  * decoder pairs its weights. */
@@ -334,6 +337,19 @@ int rwkvq_wkv7_decode_lora(const float* rkv, const float* const* h,
 int rwkvq_gemm_f16_seg(const uint16_t* w, int nseg, const int* seg_rows,
                        int in, const float* x, long x_ld, float* y, int M,
                        int seg_modes, int flags, void* stream);
+
+/* Up to 8 independent dense fp16 GEMMs in one launch: segment j computes
+ * y[j][t * rows[j] + r] = epi_j(sum_c x_j[t * x_ld[j] + c] * w[j][r * in[j]
+ * + c]) for t < M, r < rows[j] (a multiple of 128), c < in[j] (a multiple
+ * of 128); epi_j = 4-bit field j of seg_modes.  flags as for
+ * rwkvq_gemm_f16_seg (RWKVQ_X_F16: x_j fp16 in natural pair order).
+ * Replaces: the up products of QuantTMix._lora in prefill, one matmul per
+ * branch in the reference (quant_model.py:462-526), here one launch. */
+int rwkvq_gemm_f16_grouped(int nseg, const uint16_t* const* w,
+                           const int* rows, const int* in,
+                           const void* const* x, const long* x_ld,
+                           float* const* y, int M, int seg_modes, int flags,
+                           void* stream);
 
 /* Dense fp16 rows in up to 8 segments of one matrix w [sum rows, in], for
  * 1..16 input rows, on the matrix cores: segment j (rows seg_rows[j], a

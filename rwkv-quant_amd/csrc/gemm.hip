@@ -67,6 +67,16 @@ struct GemmArgs {
   int* cnt;
   int xh;                // x is fp16 in the format's pair order
   int yord;              // -1: fp32 y; else fp16 y in pair order yord
+  int nosplit;           // never split K (caller runs GEMMs concurrently)
+  long ldy;              // row stride of y (elements)
+  // grouped launch (rwkvq_gemm_f16_grouped): segment j (rows of the segment
+  // table) is a matrix of its own
+  int grouped;
+  const uint8_t* gq[8];
+  const float* gx[8];
+  long gxld[8];
+  float* gy[8];
+  int gin[8], gin_rows[8];
 };
 
 constexpr int kStepK = 128;                 // columns per K step
@@ -168,7 +178,8 @@ __device__ __forceinline__ void weights_of(const Raw2& r2, int gi, int kb,
 
 template <int FMT, int WN, int WM, int KG, bool XH>
 __global__ void __launch_bounds__(256 * KG)
-gemm_kernel(GemmArgs a) {
+gemm_kernel(GemmArgs a0) {
+  GemmArgs a = a0;     // (grouped launches substitute the segment's fields)
   constexpr int BM = 32 * WM;
   constexpr int BN = 128 * WN;
   constexpr int XI = BM * 16 / 256;          // staging items per thread
@@ -198,7 +209,7 @@ gemm_kernel(GemmArgs a) {
     j = blockIdx.x / a.mt;
   }
   const int nt = j / a.split, sp = j % a.split;
-  const int n0 = nt * BN;
+  int n0 = nt * BN;
   const int m0 = mt * BM;
   int seg = n0 / a.out_per;
   if (a.nseg_tab > 0) {                    // constant-index reads only
@@ -207,12 +218,24 @@ gemm_kernel(GemmArgs a) {
     for (int j = 0; j < 7; ++j)
       seg += (j + 1 < a.nseg_tab && n0 >= a.seg_end[j]) ? 1 : 0;
   }
+  int xseg = seg;                          // x segment offset (seg * in)
+  if (a.grouped) {
+    // segment j is its own matrix: weights, K, x, y (row stride = its rows)
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (j == seg) {
+        a.q = a.gq[j]; a.in = a.gin[j]; a.x = a.gx[j]; a.x_ld = a.gxld[j];
+        a.y = a.gy[j]; a.ldy = a.gin_rows[j];
+        n0 -= j ? a.seg_end[j - 1] : 0;
+      }
+    xseg = 0;
+  }
   const int ng = a.in >> 5, nsb = a.in >> 8;
   const int nrun = a.in / kStepK / a.split;   // K steps of this workgroup
   const int c0 = sp * nrun;
-  const float* xb = a.x + (size_t)seg * a.in;
+  const float* xb = a.x + (size_t)xseg * a.in;
   // fp16 x (XH): already in pair order, x_ld in halves
-  const uint16_t* xh = reinterpret_cast<const uint16_t*>(a.x) + (size_t)seg * a.in;
+  const uint16_t* xh = reinterpret_cast<const uint16_t*>(a.x) + (size_t)xseg * a.in;
 
   // ---- x staging: item = (token, group of the step, sub-step)
   float4 xa[XH ? 1 : XI], xbv[XH ? 1 : XI];
@@ -455,7 +478,7 @@ gemm_kernel(GemmArgs a) {
   for (int mi = 0; mi < WM; ++mi) {
     const int t = m0 + mi * 32 + r;
     if (t >= a.M) continue;
-    float* yrow = a.y + (size_t)t * a.N;
+    float* yrow = a.y + (size_t)t * a.ldy;
 #pragma unroll
     for (int ni = 0; ni < WN; ++ni) {
       const int nb = n0 + wave * 32 * WN + ni * 32;   // 32-row block
@@ -502,7 +525,7 @@ gemm_kernel(GemmArgs a) {
       // fp16 output in the pair order of the consuming GEMM: the block's 32
       // rows are that GEMM's 32-column group, half 2i / 2i+1 = columns
       // (c0(i), c1(i)); a lane's rows pair up with rows it holds itself
-      uint16_t* yh = reinterpret_cast<uint16_t*>(a.y) + (size_t)t * a.N + nb;
+      uint16_t* yh = reinterpret_cast<uint16_t*>(a.y) + (size_t)t * a.ldy + nb;
       // rounded to fp32 first, as the fp32 output (no fused mixed-precision
       // multiply-add + conversion)
 #pragma unroll
@@ -605,7 +628,7 @@ int launch_gemm(const GemmArgs& a, hipStream_t s) {
   const int nsteps = a.in / kStepK;
   const bool wide = a.out_per % 256 == 0 && a.nseg_tab == 0;
   if (wide && wgs(256, 128) >= 256) return launch_tile<FMT, 2, 4>(a, s);
-  const SplitWs* ws = current_ws();
+  const SplitWs* ws = a.nosplit ? nullptr : current_ws();
   if (RWKVQ_GEMM_SPLIT && a.M > 64) {
     // Two 4-wave workgroups per CU (each with its own barrier, so the two
     // waves of a SIMD drift out of phase and overlap decode with MFMA)
@@ -634,12 +657,26 @@ int launch_gemm(const GemmArgs& a, hipStream_t s) {
   }
   if (wide && wgs(256, 64) >= 256) return launch_tile<FMT, 2, 2>(a, s);
   if (wgs(128, 64) >= 256) return launch_tile<FMT, 1, 2>(a, s);
+  if (RWKVQ_GEMM_SPLIT && wgs(128, 32) < 256 && a.M > 32 && nsteps >= 4 &&
+      ws) {
+    // few output tiles even at 128 x 32 (e.g. the LoRA down products):
+    // 128 x 64 tiles split into runs of >= 2 steps
+    const long t = wgs(128, 64);
+    int split = 1;
+    while (t * split < 256 && split < 8 && nsteps % (4 * split) == 0 &&
+           t <= ws->ncnt &&
+           t * 2 * split * 128 * 64 * (long)sizeof(float) <= ws->bytes)
+      split *= 2;
+    if (split > 1 && t * split >= 192)
+      return launch_tile<FMT, 1, 2>(a, s, split, ws);
+  }
   return launch_tile<FMT, 1, 1>(a, s);
 }
 
 int check_gemm(int rows, int in, int out_per, int M, long x_ld, int mode,
                int k_mult = 256) {
-  if (mode & ~(15 | RWKVQ_X_F16 | RWKVQ_Y_F16 | (3 << RWKVQ_Y_ORDER_SHIFT)))
+  if (mode & ~(15 | RWKVQ_X_F16 | RWKVQ_Y_F16 | (3 << RWKVQ_Y_ORDER_SHIFT) |
+               RWKVQ_NO_SPLIT))
     return RWKVQ_ERR_ARG;
   if (mode & RWKVQ_Y_F16) {                   // fp16 y: no residual add
     if (((mode >> RWKVQ_Y_ORDER_SHIFT) & 3) > RWKVQ_ORDER_SYM6 ||
@@ -668,8 +705,10 @@ GemmArgs make_args(int rows, int in, int out_per, const float* x, long x_ld,
   a.split = 1;
   a.xh = (mode & RWKVQ_X_F16) != 0;
   a.yord = (mode & RWKVQ_Y_F16) ? (mode >> RWKVQ_Y_ORDER_SHIFT) & 3 : -1;
+  a.nosplit = (mode & RWKVQ_NO_SPLIT) != 0;
   mode &= 15;
   a.x = x; a.y = y; a.M = M; a.N = rows; a.in = in; a.out_per = out_per;
+  a.ldy = rows;
   a.mode = mode;
   a.x_ld = x_ld > 0 ? x_ld : (long)(rows / out_per) * in;
   return a;
@@ -819,6 +858,7 @@ int rwkvq_gemm_f16_seg(const uint16_t* w, int nseg, const int* seg_rows,
     a.seg_end[j] = rows;
   }
   a.x = x; a.y = y; a.M = M; a.N = rows; a.in = in; a.out_per = rows;
+  a.ldy = rows;
   a.x_ld = x_ld > 0 ? x_ld : (long)nseg * in;
   if (a.x_ld < (long)nseg * in || check_x(x, a.x_ld, a.xh))
     return RWKVQ_ERR_ARG;
@@ -827,6 +867,50 @@ int rwkvq_gemm_f16_seg(const uint16_t* w, int nseg, const int* seg_rows,
   a.nseg_tab = nseg;
   a.q = reinterpret_cast<const uint8_t*>(w);
   return launch_gemm<F_F16>(a, (hipStream_t)stream);
+}
+
+int rwkvq_gemm_f16_grouped(int nseg, const uint16_t* const* w,
+                           const int* rows, const int* in,
+                           const void* const* x, const long* x_ld,
+                           float* const* y, int M, int seg_modes, int flags,
+                           void* stream) {
+  if (nseg < 1 || nseg > 8 || !w || !rows || !in || !x || !x_ld || !y ||
+      M <= 0 || (flags & 15) ||
+      check_gemm(128, 128, 128, 1, 128, flags, kStepK))
+    return RWKVQ_ERR_ARG;
+  GemmArgs a = make_args(128, 128, 128, nullptr, 0, nullptr, M, flags);
+  a.split = 1;
+  int tot = 0;
+  for (int j = 0; j < nseg; ++j) {
+    const int m = (seg_modes >> (4 * j)) & 15;
+    if (!w[j] || !x[j] || !y[j] || rows[j] <= 0 || rows[j] % 128 ||
+        in[j] <= 0 || in[j] % kStepK || x_ld[j] < in[j] ||
+        check_x(x[j], x_ld[j], a.xh) || m > RWKVQ_EPI_SIGMOID ||
+        (a.yord >= 0 && m == RWKVQ_EPI_ADD))
+      return RWKVQ_ERR_ARG;
+    a.gq[j] = reinterpret_cast<const uint8_t*>(w[j]);
+    a.gx[j] = static_cast<const float*>(x[j]);
+    a.gxld[j] = x_ld[j];
+    a.gy[j] = y[j];
+    a.gin[j] = in[j];
+    a.gin_rows[j] = rows[j];
+    tot += rows[j];
+    a.seg_end[j] = tot;
+  }
+  a.grouped = 1;
+  a.nseg_tab = nseg;
+  a.mode = RWKVQ_EPI_PER_SEG;
+  a.seg_modes = seg_modes;
+  a.N = tot; a.out_per = tot; a.in = kStepK;   // (per segment in the kernel)
+  a.q = a.gq[0]; a.x = a.gx[0]; a.y = a.gy[0];
+  hipStream_t s = (hipStream_t)stream;
+  // one workgroup per (128-row tile, token tile), one K group: the
+  // segments' step counts differ
+  auto wgs = [&](int bm) { return (long)(tot / 128) * ((M + bm - 1) / bm); };
+  if (wgs(128) >= 256)
+    return launch_tile<F_F16, 1, 4>(a, s, 1, nullptr, true);
+  if (wgs(64) >= 256) return launch_tile<F_F16, 1, 2>(a, s, 1, nullptr, true);
+  return launch_tile<F_F16, 1, 1>(a, s, 1, nullptr, true);
 }
 
 }  // extern "C"

@@ -20,6 +20,7 @@ EPI_PER_SEG = 5                # rwkvq_gemm_f16: mode per input segment
 X_F16 = 16                     # GEMM flag: x is fp16 in the format's pair order
 Y_F16 = 32                     # GEMM flag: y is fp16 in pair order (bits 6-7)
 Y_ORDER_SHIFT = 6
+NO_SPLIT = 256                 # GEMM flag: no split-K (concurrent streams)
 ORDER_PAIRS, ORDER_SB6, ORDER_SYM6 = 0, 1, 2
 
 _P = ctypes.c_void_p
@@ -41,6 +42,7 @@ SIGNATURES = {
     "rwkvq_gemv_f16_seg": [_P, _I, _P, _I, _P, _L, _P, _I, _I, _P],
     "rwkvq_gemm_f16_seg": [_P, _I, _P, _I, _P, _L, _P, _I, _I, _I, _P],
     "rwkvq_gemm_workspace": [_P, _L, _P, _I],
+    "rwkvq_gemm_f16_grouped": [_I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P],
     "rwkvq_x16": [_P, _L, _I, _I, _I, _P, _L, _P],
     "rwkvq_dequant_sb6_f32": [_P, _P, _P, _I, _I, _I, _P, _I, _P],
     "rwkvq_dequant_sym_f32": [_P, _P, _P, _P, _I, _I, _I, _P, _I, _P],

@@ -288,13 +288,17 @@ class QuantTMix:
         # the down GEMM wrote rows of `tot` values, branch j from column
         # sum(rps[:j]) on
         hc = hbuf.view(-1)[:N * tot].view(N, tot)
-        off = 0
-        for j, b in enumerate(order):
-            _lib.call("rwkvq_gemm_f16", _lib.ptr(B_pad[b]), C, rps[j], C,
-                      _lib.ptr(hc[:, off:]), tot, _lib.ptr(wk.yl[b]), N,
-                      _lib.EPI_STORE | (_lib.X_F16 if x16 else 0), 0,
-                      _stream())
-            off += rps[j]
+        # the up products, one launch: branch j reads its rps[j] columns
+        offs = [sum(rps[:j]) for j in range(nseg)]
+        P = ctypes.c_void_p
+        _lib.call("rwkvq_gemm_f16_grouped", nseg,
+                  (P * nseg)(*[B_pad[b].data_ptr() for b in order]),
+                  (ctypes.c_int * nseg)(*[C] * nseg),
+                  (ctypes.c_int * nseg)(*rps),
+                  (P * nseg)(*[hc[:, o:].data_ptr() for o in offs]),
+                  (ctypes.c_long * nseg)(*[tot] * nseg),
+                  (P * nseg)(*[wk.yl[b].data_ptr() for b in order]),
+                  N, 0, _lib.X_F16 if x16 else 0, _stream())
 
     def _prefill_mats(self, x_order=_lib.ORDER_PAIRS):
         """Prefill LoRA factors padded for the GEMM tiles (built on first

@@ -230,7 +230,8 @@ def test_gemm_f16_segment_table(M):
     off = 0
     for j, (Aj, m) in enumerate(zip(A, modes)):
         yj = torch.empty(M, rows[j], device="cuda")
-        _lib.call("rwkvq_gemm_f16", _lib.ptr(Aj.cuda()), rows[j], K, rows[j],
+        Ajd = Aj.cuda()        # (held: the launch is asynchronous)
+        _lib.call("rwkvq_gemm_f16", _lib.ptr(Ajd), rows[j], K, rows[j],
                   _lib.ptr(xd[:, 2 + j]), 6 * K, _lib.ptr(yj), M, m, 0,
                   _lib.stream_handle())
         assert torch.allclose(y[:, off:off + rows[j]], yj, rtol=1e-5,
@@ -331,3 +332,49 @@ def test_gemm_x16_input_equals_fp32_input(kind, bits, M):
     y = torch.empty_like(ref)
     lin._run("gemm", xh, y, mode=_lib.X_F16, n=M)
     assert torch.equal(y, ref)
+
+
+@pytest.mark.parametrize("M", [37, 512])
+@pytest.mark.parametrize("x16", [False, True])
+def test_gemm_f16_grouped(M, x16):
+    """Independent fp16 GEMMs of different K (the prefill LoRA up products,
+    ranks padded to 128 / 384) in one launch, each with its own x, y and
+    epilogue: within 2e-5 of the float64 product of the fp16 operands."""
+    import ctypes
+    g = torch.Generator().manual_seed(M + x16)
+    ks, rows = [128, 384, 128, 256], [256, 256, 128, 384]
+    modes = [_lib.EPI_STORE, _lib.EPI_TANH, _lib.EPI_SIGMOID, _lib.EPI_STORE]
+    W = [(torch.randn(r, k, generator=g) * 0.05).half() for r, k in
+         zip(rows, ks)]
+    xs = [torch.randn(M, k + 32, generator=g) for k in ks]   # x_ld = k + 32
+    Wd = [w.cuda() for w in W]
+    xd = [(x.half() if x16 else x).cuda() for x in xs]
+    ys = [torch.empty(M, r, device="cuda") for r in rows]
+    P, n = ctypes.c_void_p, len(ks)
+    _lib.call("rwkvq_gemm_f16_grouped", n, (P * n)(*[w.data_ptr() for w in Wd]),
+              (ctypes.c_int * n)(*rows), (ctypes.c_int * n)(*ks),
+              (P * n)(*[x.data_ptr() for x in xd]),
+              (ctypes.c_long * n)(*[k + 32 for k in ks]),
+              (P * n)(*[y.data_ptr() for y in ys]), M,
+              sum(m << (4 * j) for j, m in enumerate(modes)),
+              _lib.X_F16 if x16 else 0, _lib.stream_handle())
+    fns = {_lib.EPI_STORE: lambda v: v, _lib.EPI_TANH: np.tanh,
+           _lib.EPI_SIGMOID: lambda v: 1 / (1 + np.exp(-v))}
+    for j in range(n):
+        ref = fns[modes[j]](xs[j][:, :ks[j]].half().double().numpy()
+                            @ W[j].double().numpy().T)
+        assert relmax(ys[j].cpu().numpy(), ref) < 2e-5, j
+
+
+def test_gemm_f16_small_output_split():
+    """Few output tiles (the LoRA down products at pp512: 640 rows, K 2048)
+    take 128 x 64 tiles split along K: within 2e-5 of float64."""
+    g = torch.Generator().manual_seed(9)
+    A = (torch.randn(640, 2048, generator=g) * 0.05).half()
+    x = torch.randn(512, 2048, generator=g)
+    y = torch.empty(512, 640, device="cuda")
+    Ad, xd = A.cuda(), x.cuda()   # (held: the launch is asynchronous)
+    _lib.call("rwkvq_gemm_f16", _lib.ptr(Ad), 640, 2048, 640, _lib.ptr(xd),
+              0, _lib.ptr(y), 512, _lib.EPI_STORE, 0, _lib.stream_handle())
+    ref = x.half().double().numpy() @ A.double().numpy().T
+    assert relmax(y.cpu().numpy(), ref) < 2e-5

@@ -136,9 +136,10 @@ def test_wkv7_scan_chunked_in_place_and_vs_steps():
     st2 = torch.empty_like(st)
     y2 = torch.empty_like(y1)
     D = H * 64
+    s0d = s0.cuda()            # (held: the launch is asynchronous)
     _lib.call("rwkvq_wkv7_scan", _lib.ptr(dev[0]), D, _lib.ptr(dev[1]),
               _lib.ptr(dev[2]), _lib.ptr(dev[3]), _lib.ptr(dev[4]),
-              _lib.ptr(dev[5]), D, _lib.ptr(s0.cuda()), _lib.ptr(st2),
+              _lib.ptr(dev[5]), D, _lib.ptr(s0d), _lib.ptr(st2),
               _lib.ptr(y2), D, B, T, H, 64, _lib.stream_handle())
     assert torch.isfinite(y1).all() and torch.isfinite(st).all()
     assert float((y1 - y2).abs().max()) < 1e-5 * float(y2.abs().max())
