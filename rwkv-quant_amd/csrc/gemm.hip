@@ -176,13 +176,14 @@ __device__ __forceinline__ void weights_of(const Raw2& r2, int gi, int kb,
   }
 }
 
-template <int FMT, int WN, int WM, int KG, bool XH>
-__global__ void __launch_bounds__(256 * KG)
+template <int FMT, int WN, int WM, int KG, bool XH, int NW>
+__global__ void __launch_bounds__(64 * NW * KG)
 gemm_kernel(GemmArgs a0) {
   GemmArgs a = a0;     // (grouped launches substitute the segment's fields)
   constexpr int BM = 32 * WM;
-  constexpr int BN = 128 * WN;
-  constexpr int XI = BM * 16 / 256;          // staging items per thread
+  constexpr int BN = 32 * NW * WN;           // NW waves along N
+  constexpr int NT = 64 * NW;                // threads of a K group
+  constexpr int XI = BM * 16 / NT;           // staging items per thread
   // KG groups of 4 waves share the tile and split its K steps (group g
   // takes steps g, g + KG, ...): KG waves per SIMD hide each other's
   // latency without a smaller tile; the groups' sums meet in LDS at the end
@@ -190,8 +191,8 @@ gemm_kernel(GemmArgs a0) {
 
   const int lane = threadIdx.x & 63;
   const int wave_all = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int kg = wave_all >> 2, wave = wave_all & 3;
-  const int tid = threadIdx.x & 255;         // thread index in the group
+  const int kg = wave_all / NW, wave = wave_all % NW;
+  const int tid = threadIdx.x % NT;          // thread index in the group
   const int r = lane & 31, h = lane >> 5;
   // Tile order: workgroup b runs on XCD b % 8 (round-robin dispatch).  The
   // M tiles of one N tile go to the same XCD back to back, so that XCD's L2
@@ -243,7 +244,7 @@ gemm_kernel(GemmArgs a0) {
   auto load_x = [&](int c) {
 #pragma unroll
     for (int p = 0; p < XI; ++p) {
-      const int it = tid + 256 * p;
+      const int it = tid + NT * p;
       const int t = min(m0 + (it >> 4), a.M - 1);
       if constexpr (XH) {
         xq[p] = ld16(xh + (size_t)t * a.x_ld + c * kStepK + (it & 15) * 8);
@@ -260,7 +261,7 @@ gemm_kernel(GemmArgs a0) {
   auto store_x = [&](int buf) {
 #pragma unroll
     for (int p = 0; p < XI; ++p) {
-      const int it = tid + 256 * p;
+      const int it = tid + NT * p;
       const int tl = it >> 4, gq = (it >> 2) & 3, s = it & 3;
       *reinterpret_cast<uint4*>(&sx[kg][buf][tl * kRowH + gq * 32 + s * 8]) =
           XH ? xq[p] : x_pairs<FMT>(xa[p], xbv[p]);
@@ -361,7 +362,7 @@ gemm_kernel(GemmArgs a0) {
     // loop ended on a barrier); 4 waves x 16 WM WN floats x 64 lanes
     // fits them for every tile of this kernel
     constexpr int NA = WM * WN * 16;
-    static_assert(4 * NA * 64 * 4 <= (int)sizeof(sx), "reduction buffer");
+    static_assert(NW * NA * 64 * 4 <= (int)sizeof(sx), "reduction buffer");
     float* red = reinterpret_cast<float*>(&sx[0][0][0]);
     if (kg == 1) {
 #pragma unroll
@@ -394,7 +395,7 @@ gemm_kernel(GemmArgs a0) {
     // across the XCDs' L2s by themselves; a device-scope fence instead
     // would write back and invalidate the whole L2 in every workgroup.
     constexpr int NA = WM * WN * 16;
-    constexpr int TE = 4 * NA * 64;            // floats per partial tile
+    constexpr int TE = NW * NA * 64;           // floats per partial tile
     const int tile = nt * a.mt + mt;
     float* part = a.ws + (size_t)tile * a.split * TE;
     if (kg == 0) {
@@ -585,39 +586,40 @@ const SplitWs* current_ws() {
 
 // Two K groups (8 waves) wherever the tile's registers allow two waves per
 // SIMD (all tiles but 256 x 128) and the step count is even.
-template <int FMT, int WN, int WM>
+template <int FMT, int WN, int WM, int NW = 4>
 int launch_tile(const GemmArgs& a, hipStream_t s, int split = 1,
                 const SplitWs* ws = nullptr, bool one_group = false) {
   GemmArgs b = a;
-  b.nt = a.N / (128 * WN);
+  b.nt = a.N / (32 * NW * WN);
   b.mt = (a.M + 32 * WM - 1) / (32 * WM);
   b.split = split;
   if (split > 1) { b.ws = ws->ws; b.cnt = ws->cnt; }
   const int grid = b.nt * b.mt * split;
-  constexpr bool two = RWKVQ_GEMM_KG == 2 && WN * WM <= 4;
+  constexpr bool two = RWKVQ_GEMM_KG == 2 && WN * WM <= 4 && NW == 4;
   constexpr int KG2 = two ? 2 : 1;
   if (two && !one_group && (a.in / kStepK / split) % 2 == 0) {
     if (a.xh)
-      hipLaunchKernelGGL((gemm_kernel<FMT, WN, WM, KG2, true>), dim3(grid),
-                         dim3(512), 0, s, b);
+      hipLaunchKernelGGL((gemm_kernel<FMT, WN, WM, KG2, true, NW>),
+                         dim3(grid), dim3(64 * NW * KG2), 0, s, b);
     else
-      hipLaunchKernelGGL((gemm_kernel<FMT, WN, WM, KG2, false>), dim3(grid),
-                         dim3(512), 0, s, b);
+      hipLaunchKernelGGL((gemm_kernel<FMT, WN, WM, KG2, false, NW>),
+                         dim3(grid), dim3(64 * NW * KG2), 0, s, b);
   } else {
     if (a.xh)
-      hipLaunchKernelGGL((gemm_kernel<FMT, WN, WM, 1, true>), dim3(grid),
-                         dim3(256), 0, s, b);
+      hipLaunchKernelGGL((gemm_kernel<FMT, WN, WM, 1, true, NW>), dim3(grid),
+                         dim3(64 * NW), 0, s, b);
     else
-      hipLaunchKernelGGL((gemm_kernel<FMT, WN, WM, 1, false>), dim3(grid),
-                         dim3(256), 0, s, b);
+      hipLaunchKernelGGL((gemm_kernel<FMT, WN, WM, 1, false, NW>),
+                         dim3(grid), dim3(64 * NW), 0, s, b);
   }
   return hipGetLastError() == hipSuccess ? RWKVQ_OK : RWKVQ_ERR_LAUNCH;
 }
 
-// Tile choice: 256 x 128 (a wave: 64 rows x 128 tokens) where that alone
-// gives >= 256 workgroups; else 128 x 128 (a wave: 32 rows x 128 tokens,
-// each decoded weight feeds 4 MFMAs), split along K where that fills the
-// chip; else the largest smaller tile that still gives >= 256 workgroups.
+// Tile choice: 256 x 128 (8 waves of 32 rows x 128 tokens) where that
+// alone gives >= 256 workgroups; else 128 x 128 (4 waves of 32 rows x 128
+// tokens, each decoded weight feeds 4 MFMAs), split along K where that
+// fills the chip; else the largest smaller tile that still gives >= 256
+// workgroups.
 // N tiles of 256 rows need out_per % 256 == 0; segment tables take 128-row
 // tiles (their segments are multiples of 128 rows).
 template <int FMT>
@@ -627,8 +629,10 @@ int launch_gemm(const GemmArgs& a, hipStream_t s) {
   };
   const int nsteps = a.in / kStepK;
   const bool wide = a.out_per % 256 == 0 && a.nseg_tab == 0;
-  if (wide && wgs(256, 128) >= 256) return launch_tile<FMT, 2, 4>(a, s);
   const SplitWs* ws = a.nosplit ? nullptr : current_ws();
+  // 256 x 128 tiles of 8 waves (32 rows x 128 tokens each; x staged once
+  // for 256 rows) where they alone give >= 256 workgroups
+  if (wide && wgs(256, 128) >= 256) return launch_tile<FMT, 1, 4, 8>(a, s);
   if (RWKVQ_GEMM_SPLIT && a.M > 64) {
     // Two 4-wave workgroups per CU (each with its own barrier, so the two
     // waves of a SIMD drift out of phase and overlap decode with MFMA)
