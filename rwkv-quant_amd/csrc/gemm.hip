@@ -34,6 +34,8 @@
 //   sb6   w = fma(q, f16(s), f16(m))   (s = max(f32(f16(qs*d)), 1e-8))
 //   sym   w = q * f16(qs * d)
 //   rtn8  w = q, the fp32 row scale multiplies the fp32 sum
+#include <type_traits>
+
 #include "qfmt.h"
 #include "rwkvq_hip.h"
 
@@ -221,14 +223,27 @@ gemm_kernel(GemmArgs a0) {
   }
   int xseg = seg;                          // x segment offset (seg * in)
   if (a.grouped) {
-    // segment j is its own matrix: weights, K, x, y (row stride = its rows)
+    // segment j is its own matrix: weights, K, x, y (row stride = its rows);
+    // chosen by selects over constant indices (kernel arguments stay in
+    // SGPRs)
+    const uint8_t* q = a0.gq[0];
+    const float* x = a0.gx[0];
+    float* y = a0.gy[0];
+    long xld = a0.gxld[0];
+    int in = a0.gin[0], ldy = a0.gin_rows[0], off = 0;
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (j == seg) {
-        a.q = a.gq[j]; a.in = a.gin[j]; a.x = a.gx[j]; a.x_ld = a.gxld[j];
-        a.y = a.gy[j]; a.ldy = a.gin_rows[j];
-        n0 -= j ? a.seg_end[j - 1] : 0;
-      }
+    for (int j = 1; j < 8; ++j) {
+      const bool m = j == seg;
+      q = m ? a0.gq[j] : q;
+      x = m ? a0.gx[j] : x;
+      y = m ? a0.gy[j] : y;
+      xld = m ? a0.gxld[j] : xld;
+      in = m ? a0.gin[j] : in;
+      ldy = m ? a0.gin_rows[j] : ldy;
+      off = m ? a0.seg_end[j - 1] : off;
+    }
+    a.q = q; a.x = x; a.y = y; a.x_ld = xld; a.in = in; a.ldy = ldy;
+    n0 -= off;
     xseg = 0;
   }
   const int ng = a.in >> 5, nsb = a.in >> 8;
@@ -273,7 +288,6 @@ gemm_kernel(GemmArgs a0) {
 #pragma unroll
   for (int ni = 0; ni < WN; ++ni)
     rows[ni] = n0 + wave * 32 * WN + ni * 32 + r;
-  Raw2 cur[WN], nxt[WN];
   auto load_w = [&](int c, Raw2 (&dst)[WN]) {
 #pragma unroll
     for (int ni = 0; ni < WN; ++ni)
@@ -288,17 +302,24 @@ gemm_kernel(GemmArgs a0) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[mi][ni][v] = 0.f;
 
-  load_w(c0 + kg, cur);
+  // Weights are fetched two steps ahead, into ping-pong register sets: the
+  // set of step i is refilled with step i + 2 as soon as its second group
+  // is decoded, so an HBM fetch has about a step and a half to land.  x is
+  // fetched one step ahead (it comes from L2).
+  const int clast = c0 + nrun - KG + kg;       // the group's last step
+  Raw2 wset[2][WN];
+  load_w(c0 + kg, wset[0]);
+  load_w(min(c0 + KG + kg, clast), wset[1]);
   load_x(c0 + kg);
   store_x(0);
   __syncthreads();
 
   const int nsg = nrun / KG;                   // steps of each group
-  for (int i = 0; i < nsg; ++i) {
+  auto step = [&](int i, auto set_tag) __attribute__((always_inline)) {
+    constexpr int S = decltype(set_tag)::value;   // register set of step i
     const int c = c0 + i * KG + kg;
     // clamped to the group's last step: loads stay in W / x
-    const int cn = min(c + KG, c0 + nrun - KG + kg);
-    load_w(cn, nxt);
+    const int cn = min(c + KG, clast), cnn = min(c + 2 * KG, clast);
     load_x(cn);
     // keep the loads of step c + KG ahead of this step's MFMAs: left to
     // itself the scheduler sinks them next to their use
@@ -320,7 +341,7 @@ gemm_kernel(GemmArgs a0) {
     read_bx(0, bx[0]);
 #pragma unroll
     for (int ni = 0; ni < WN; ++ni)
-      weights_of<FMT>(cur[ni], 0, (c * 4 + 2 * h) & 7, w[0][ni]);
+      weights_of<FMT>(wset[S][ni], 0, (c * 4 + 2 * h) & 7, w[0][ni]);
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       const int gi = k >> 2, ss = k & 3;
@@ -328,7 +349,11 @@ gemm_kernel(GemmArgs a0) {
       if (k == 1) {
 #pragma unroll
         for (int ni = 0; ni < WN; ++ni)
-          weights_of<FMT>(cur[ni], 1, (c * 4 + 2 * h + 1) & 7, w[1][ni]);
+          weights_of<FMT>(wset[S][ni], 1, (c * 4 + 2 * h + 1) & 7, w[1][ni]);
+        // the set is decoded: refill it with step c + 2 KG
+        __builtin_amdgcn_sched_barrier(0);
+        load_w(cnn, wset[S]);
+        __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
       for (int ni = 0; ni < WN; ++ni) {
@@ -342,19 +367,19 @@ gemm_kernel(GemmArgs a0) {
               av, bx[k & 1][mi], acc[mi][ni], 0, 0, 0);
       }
     }
-    // the prefetched registers are consumed only from here on
+    // the prefetched x registers are consumed only from here on
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int p = 0; p < XI; ++p) {
       if constexpr (XH) pin(xq[p]);
       else { pin(xa[p]); pin(xbv[p]); }
     }
-#pragma unroll
-    for (int ni = 0; ni < WN; ++ni) pin_raw2<FMT>(nxt[ni]);
     store_x((i + 1) & 1);
     __syncthreads();
-#pragma unroll
-    for (int ni = 0; ni < WN; ++ni) cur[ni] = nxt[ni];
+  };
+  for (int i = 0; i < nsg; i += 2) {
+    step(i, std::integral_constant<int, 0>());
+    if (i + 1 < nsg) step(i + 1, std::integral_constant<int, 1>());
   }
 
   if constexpr (KG > 1) {
