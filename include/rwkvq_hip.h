@@ -338,6 +338,23 @@ int rwkvq_gemm_f16_seg(const uint16_t* w, int nseg, const int* seg_rows,
                        int in, const float* x, long x_ld, float* y, int M,
                        int seg_modes, int flags, void* stream);
 
+/* A quantized GEMM (as rwkvq_gemm_sb6 / _sym / _rtn8: kind 0 sb6 with p0..p2
+ * = nib, hb, rec; kind 1 sym with p0..p3 = codes, hb, qs, d; kind 2 rtn8
+ * with p0 = codes, p3 = scale) and a segmented fp16 GEMM of the same K
+ * (as rwkvq_gemm_f16_seg: w, nseg, seg_rows, xb, xb_ld, yb, seg_modes,
+ * flags_b) over the same M tokens, in one launch when the first leaves CUs
+ * free (both inputs RWKVQ_X_F16), else as two launches.  Replaces: the
+ * prefill r/k/v projections and the LoRA down products of the time mix,
+ * which read the same lerp outputs (reference: quant_model.py:462-526,
+ * 643-650). */
+int rwkvq_gemm_dual_f16seg(int kind, int bits, const void* p0, const void* p1,
+                           const void* p2, const void* p3, int rows, int in,
+                           int out_per, const void* x, long x_ld, float* y,
+                           int mode, const uint16_t* w, int nseg,
+                           const int* seg_rows, const void* xb, long xb_ld,
+                           float* yb, int seg_modes, int flags_b, int M,
+                           void* stream);
+
 /* Up to 8 independent dense fp16 GEMMs in one launch: segment j computes
  * y[j][t * rows[j] + r] = epi_j(sum_c x_j[t * x_ld[j] + c] * w[j][r * in[j]
  * + c]) for t < M, r < rows[j] (a multiple of 128), c < in[j] (a multiple

@@ -178,18 +178,22 @@ __device__ __forceinline__ void weights_of(const Raw2& r2, int gi, int kb,
   }
 }
 
+// The workgroup's x staging buffers: KG groups x 2 steps x BM rows.
+template <int WM, int KG>
+using XStage = _Float16[KG][2][32 * WM * kRowH];
+
+// One workgroup's tile (bid: its index in the launch).  KG groups of NW
+// waves share the tile and split its K steps (group g takes steps g,
+// g + KG, ...): KG waves per SIMD hide each other's latency without a
+// smaller tile; the groups' sums meet in LDS at the end.
 template <int FMT, int WN, int WM, int KG, bool XH, int NW>
-__global__ void __launch_bounds__(64 * NW * KG)
-gemm_kernel(GemmArgs a0) {
+__device__ __forceinline__ void gemm_tile(const GemmArgs& a0, const int bid,
+                                          XStage<WM, KG>& sx) {
   GemmArgs a = a0;     // (grouped launches substitute the segment's fields)
   constexpr int BM = 32 * WM;
   constexpr int BN = 32 * NW * WN;           // NW waves along N
   constexpr int NT = 64 * NW;                // threads of a K group
   constexpr int XI = BM * 16 / NT;           // staging items per thread
-  // KG groups of 4 waves share the tile and split its K steps (group g
-  // takes steps g, g + KG, ...): KG waves per SIMD hide each other's
-  // latency without a smaller tile; the groups' sums meet in LDS at the end
-  __shared__ __attribute__((aligned(16))) _Float16 sx[KG][2][BM * kRowH];
 
   const int lane = threadIdx.x & 63;
   const int wave_all = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -204,12 +208,12 @@ gemm_kernel(GemmArgs a0) {
   // of one (N tile, K run) share an XCD, the runs of a tile spread out.
   int j, mt;
   if (((a.nt * a.split) & 7) == 0) {
-    const int slot = blockIdx.x >> 3;
+    const int slot = bid >> 3;
     mt = slot % a.mt;
-    j = (slot / a.mt) * 8 + (blockIdx.x & 7);
+    j = (slot / a.mt) * 8 + (bid & 7);
   } else {
-    mt = blockIdx.x % a.mt;
-    j = blockIdx.x / a.mt;
+    mt = bid % a.mt;
+    j = bid / a.mt;
   }
   const int nt = j / a.split, sp = j % a.split;
   int n0 = nt * BN;
@@ -579,6 +583,28 @@ gemm_kernel(GemmArgs a0) {
   }
 }
 
+template <int FMT, int WN, int WM, int KG, bool XH, int NW>
+__global__ void __launch_bounds__(64 * NW * KG)
+gemm_kernel(GemmArgs a) {
+  __shared__ __attribute__((aligned(16))) XStage<WM, KG> sx;
+  gemm_tile<FMT, WN, WM, KG, XH, NW>(a, blockIdx.x, sx);
+}
+
+// Two GEMMs of the same tile shape in one launch: workgroups [0, grid_a)
+// run GEMM a (format FA), the rest GEMM b (format FB) -- the prefill r/k/v
+// projection and the LoRA down products, which read the same lerp outputs
+// and have the same K, so the few down tiles run on the CUs the r/k/v
+// tiles leave free instead of after them.
+template <int FA, int FB, int WN, int WM, int KG, bool XH, int NW>
+__global__ void __launch_bounds__(64 * NW * KG)
+gemm_dual_kernel(GemmArgs a, GemmArgs b, int grid_a) {
+  __shared__ __attribute__((aligned(16))) XStage<WM, KG> sx;
+  if ((int)blockIdx.x < grid_a)
+    gemm_tile<FA, WN, WM, KG, XH, NW>(a, blockIdx.x, sx);
+  else
+    gemm_tile<FB, WN, WM, KG, XH, NW>(b, blockIdx.x - grid_a, sx);
+}
+
 #ifndef RWKVQ_GEMM_KG
 #define RWKVQ_GEMM_KG 2
 #endif
@@ -896,6 +922,112 @@ int rwkvq_gemm_f16_seg(const uint16_t* w, int nseg, const int* seg_rows,
   a.nseg_tab = nseg;
   a.q = reinterpret_cast<const uint8_t*>(w);
   return launch_gemm<F_F16>(a, (hipStream_t)stream);
+}
+
+int rwkvq_gemm_dual_f16seg(int kind, int bits, const void* p0, const void* p1,
+                           const void* p2, const void* p3, int rows, int in,
+                           int out_per, const void* x, long x_ld, float* y,
+                           int mode, const uint16_t* w, int nseg,
+                           const int* seg_rows, const void* xb, long xb_ld,
+                           float* yb, int seg_modes, int flags_b, int M,
+                           void* stream) {
+  hipStream_t s = (hipStream_t)stream;
+  // GEMM a: the quantized projection, as rwkvq_gemm_{sb6,sym,rtn8}
+  GemmArgs a = make_args(rows, in, out_per, static_cast<const float*>(x),
+                         x_ld, y, M, mode);
+  int st = check_gemm(rows, in, out_per, M, a.x_ld, mode);
+  if (!st) st = check_x(x, a.x_ld, a.xh);
+  if (st) return st;
+  int fa;
+  if (kind == 0) {                               // sb6: nib, hb, rec
+    if (bits < 4 || bits > 6 || (bits > 4 && !p1) || !p0 || !p2)
+      return RWKVQ_ERR_ARG;
+    a.q = static_cast<const uint8_t*>(p0);
+    a.hb = static_cast<const uint32_t*>(p1);
+    a.rec = static_cast<const uint8_t*>(p2);
+    fa = bits == 4 ? F_SB6_4 : bits == 5 ? F_SB6_5 : F_SB6_6;
+  } else if (kind == 1) {                        // sym: codes, hb, qs, d
+    if ((bits != 6 && bits != 8) || (bits == 6 && !p1) || !p0 || !p2 || !p3)
+      return RWKVQ_ERR_ARG;
+    a.q = static_cast<const uint8_t*>(p0);
+    a.hb = static_cast<const uint32_t*>(p1);
+    a.qs = static_cast<const int8_t*>(p2);
+    a.d = static_cast<const uint16_t*>(p3);
+    fa = bits == 6 ? F_SYM6 : F_SYM8;
+  } else if (kind == 2) {                        // rtn8: codes, scale
+    if (bits != 8 || !p0 || !p3) return RWKVQ_ERR_ARG;
+    a.q = static_cast<const uint8_t*>(p0);
+    a.d = static_cast<const uint16_t*>(p3);
+    fa = F_RTN8;
+  } else {
+    return RWKVQ_ERR_ARG;
+  }
+  // GEMM b: the segmented fp16 GEMM, as rwkvq_gemm_f16_seg
+  if (!w || !xb || !yb || nseg < 1 || nseg > 8 || in % kStepK ||
+      (flags_b & 15) || check_gemm(128, 128, 128, 1, 128, flags_b, kStepK))
+    return RWKVQ_ERR_ARG;
+  GemmArgs b = make_args(128, 128, 128, static_cast<const float*>(xb), xb_ld,
+                         yb, M, flags_b);
+  int rows_b = 0;
+  for (int j = 0; j < nseg; ++j) {
+    const int m = (seg_modes >> (4 * j)) & 15;
+    if (seg_rows[j] <= 0 || seg_rows[j] % 128 || m > RWKVQ_EPI_SIGMOID ||
+        (b.yord >= 0 && m == RWKVQ_EPI_ADD))
+      return RWKVQ_ERR_ARG;
+    rows_b += seg_rows[j];
+    b.seg_end[j] = rows_b;
+  }
+  b.x = static_cast<const float*>(xb); b.y = yb; b.N = rows_b; b.in = in;
+  b.out_per = rows_b; b.ldy = rows_b;
+  b.x_ld = xb_ld > 0 ? xb_ld : (long)nseg * in;
+  if (b.x_ld < (long)nseg * in || check_x(xb, b.x_ld, b.xh))
+    return RWKVQ_ERR_ARG;
+  b.mode = RWKVQ_EPI_PER_SEG;
+  b.seg_modes = seg_modes;
+  b.nseg_tab = nseg;
+  b.q = reinterpret_cast<const uint8_t*>(w);
+
+  // One launch of 128 x 128 tiles (two K groups, no split) when GEMM a
+  // leaves CUs free; otherwise the two GEMMs as separate launches.
+  const long mt = (M + 127) / 128;
+  const long ta = (rows / 128) * mt, tb = (rows_b / 128) * mt;
+  const bool dual = a.xh && b.xh && M > 64 && (in / kStepK) % 2 == 0 &&
+                    ta < 256;
+  if (!dual) {
+    auto one = [&](int f, const GemmArgs& g) {
+      switch (f) {
+        case F_SB6_4: return launch_gemm<F_SB6_4>(g, s);
+        case F_SB6_5: return launch_gemm<F_SB6_5>(g, s);
+        case F_SB6_6: return launch_gemm<F_SB6_6>(g, s);
+        case F_SYM6: return launch_gemm<F_SYM6>(g, s);
+        case F_SYM8: return launch_gemm<F_SYM8>(g, s);
+        case F_RTN8: return launch_gemm<F_RTN8>(g, s);
+        default: return launch_gemm<F_F16>(g, s);
+      }
+    };
+    st = one(fa, a);
+    return st ? st : one(F_F16, b);
+  }
+  a.split = b.split = 1;
+  a.nt = rows / 128; b.nt = rows_b / 128;
+  a.mt = b.mt = (int)mt;
+  const dim3 grid((unsigned)(ta + tb)), block(512);
+  switch (fa) {
+#define RWKVQ_DUAL(F)                                                        \
+  case F:                                                                    \
+    hipLaunchKernelGGL((gemm_dual_kernel<F, F_F16, 1, 4, 2, true, 4>), grid, \
+                       block, 0, s, a, b, (int)ta);                          \
+    break;
+    RWKVQ_DUAL(F_SB6_4)
+    RWKVQ_DUAL(F_SB6_5)
+    RWKVQ_DUAL(F_SB6_6)
+    RWKVQ_DUAL(F_SYM6)
+    RWKVQ_DUAL(F_SYM8)
+    RWKVQ_DUAL(F_RTN8)
+#undef RWKVQ_DUAL
+    default: return RWKVQ_ERR_ARG;
+  }
+  return hipGetLastError() == hipSuccess ? RWKVQ_OK : RWKVQ_ERR_LAUNCH;
 }
 
 int rwkvq_gemm_f16_grouped(int nseg, const uint16_t* const* w,

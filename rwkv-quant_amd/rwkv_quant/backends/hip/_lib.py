@@ -43,6 +43,8 @@ SIGNATURES = {
     "rwkvq_gemm_f16_seg": [_P, _I, _P, _I, _P, _L, _P, _I, _I, _I, _P],
     "rwkvq_gemm_workspace": [_P, _L, _P, _I],
     "rwkvq_gemm_f16_grouped": [_I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P],
+    "rwkvq_gemm_dual_f16seg": [_I, _I, _P, _P, _P, _P, _I, _I, _I, _P, _L, _P,
+                               _I, _P, _I, _P, _P, _L, _P, _I, _I, _I, _P],
     "rwkvq_x16": [_P, _L, _I, _I, _I, _P, _L, _P],
     "rwkvq_dequant_sb6_f32": [_P, _P, _P, _I, _I, _I, _P, _I, _P],
     "rwkvq_dequant_sym_f32": [_P, _P, _P, _P, _I, _I, _I, _P, _I, _P],

@@ -287,8 +287,43 @@ class QuantTMix:
                   modes, flags, _stream())
         # the down GEMM wrote rows of `tot` values, branch j from column
         # sum(rps[:j]) on
+        self._run_ups(wk, x16, order, rps, B_pad)
+
+    def run_rkv_lora_x16(self, wk, x_order):
+        """Prefill with fp16 lerp outputs (pair order x_order): the r/k/v
+        projection and the LoRA down products in one launch (the down
+        tiles run on the CUs the r/k/v tiles leave free), then the ups."""
+        N, C = wk.N, self.C
+        rf = self.rkv_fused
+        kind, lead = rf._cat._kargs()
+        if kind == "sb6":
+            k, (p0, p1, p2, bits), p3 = 0, lead, None
+        elif kind == "sym":
+            k, (p0, p1, p2, p3, bits) = 1, lead
+        else:
+            k, (p0, p3), p1, p2, bits = 2, lead, None, None, 8
+        order, rps, A_cat, B_pad, modes = self._prefill_mats(x_order)
+        xs_flat = wk.xs16.view(N, 6 * C)
+        nseg = len(order)
+        _lib.call("rwkvq_gemm_dual_f16seg", k, bits, p0, p1, p2, p3,
+                  rf.out_features, rf.in_features, rf.out_per,
+                  _lib.ptr(wk.xs16), 6 * C, _lib.ptr(wk.rkv), _lib.X_F16,
+                  _lib.ptr(A_cat), nseg, (ctypes.c_int * nseg)(*rps),
+                  _lib.ptr(xs_flat[:, self.SLOT[order[0]] * C:]), 6 * C,
+                  _lib.ptr(wk.h16), modes,
+                  _lib.X_F16 | _lib.Y_F16
+                  | (_lib.ORDER_PAIRS << _lib.Y_ORDER_SHIFT), N, _stream())
+        self._run_ups(wk, True, order, rps, B_pad)
+
+    def _run_ups(self, wk, x16, order, rps, B_pad):
+        """The up products of all branches in one launch, from the down
+        outputs (wk.h16 fp16 or wk.h_cat fp32, branch j from column
+        sum(rps[:j]) on, rows of sum(rps) values)."""
+        N, C = wk.N, self.C
+        nseg, tot = len(order), sum(rps)
+        hbuf = wk.h16 if x16 else wk.h_cat
         hc = hbuf.view(-1)[:N * tot].view(N, tot)
-        # the up products, one launch: branch j reads its rps[j] columns
+        # branch j reads its rps[j] columns
         offs = [sum(rps[:j]) for j in range(nseg)]
         P = ctypes.c_void_p
         _lib.call("rwkvq_gemm_f16_grouped", nseg,
@@ -618,8 +653,7 @@ class QuantRWKV7:
         _lib.call("rwkvq_shift_lerp_f16", _lib.ptr(x), _lib.ptr(blk.ln1_w),
                   _lib.ptr(blk.ln1_b), _lib.ptr(tshift), _lib.ptr(tm.coef), 6,
                   _lib.ptr(wk.xs16), o_r, _lib.ptr(tshift_out), B, T, C, st)
-        tm.rkv_fused.apply_into(wk.xs16, wk.rkv, N, 6 * C, mode=_lib.X_F16)
-        tm.run_lora(wk, x16_order=o_r)
+        tm.run_rkv_lora_x16(wk, o_r)
         self._wkv_seq(tm, wk, wkv_in, wkv_out, layer0, B, T, st, o16=o_o)
         tm.o_proj.apply_into(wk.o16, x, mode=_lib.EPI_ADD | _lib.X_F16, n=N)
         _lib.call("rwkvq_shift_lerp_f16", _lib.ptr(x), _lib.ptr(blk.ln2_w),

@@ -378,3 +378,48 @@ def test_gemm_f16_small_output_split():
               0, _lib.ptr(y), 512, _lib.EPI_STORE, 0, _lib.stream_handle())
     ref = x.half().double().numpy() @ A.double().numpy().T
     assert relmax(y.cpu().numpy(), ref) < 2e-5
+
+
+@pytest.mark.parametrize("kind,bits", [("sym", 8), ("sb6", 5), ("sym", 6)])
+def test_gemm_dual_equals_two_launches(kind, bits):
+    """The prefill r/k/v projection and the LoRA down products in one launch
+    (rwkvq_gemm_dual_f16seg) == the two GEMMs launched on their own: the
+    quantized one bit for bit (same tiles), the fp16 one to 1e-5 (its own
+    launch may split K)."""
+    import ctypes
+    from rwkv_quant.backends.hip.quant_linear import (GwQuantLinearFused,
+                                                       SymQuantLinearFused)
+    T, C = 512, 2048
+    lins = [LIN[kind](qt_for(kind, bits, _w(C, C, seed=40 + s)))
+            for s in range(3)]
+    fused = (GwQuantLinearFused if kind == "sb6" else SymQuantLinearFused)(lins)
+    order = _order_of(kind, bits)
+    g = torch.Generator().manual_seed(41)
+    xs = torch.randn(T, 6, C, generator=g).cuda()
+    xs16 = _to_x16(xs.view(T * 6, C), order).view(T, 6, C)
+    rows = [128, 128, 128, 256]
+    A = (torch.randn(sum(rows), C, generator=g) * 0.05).half().cuda()
+    modes = sum(m << (4 * j) for j, m in enumerate(
+        [_lib.EPI_STORE, _lib.EPI_TANH, _lib.EPI_STORE, _lib.EPI_SIGMOID]))
+    fl = _lib.X_F16 | _lib.Y_F16 | (_lib.ORDER_PAIRS << _lib.Y_ORDER_SHIFT)
+    ra = (ctypes.c_int * 4)(*rows)
+    y1 = torch.empty(T, 3 * C, device="cuda")
+    h1 = torch.empty(T, sum(rows), dtype=torch.float16, device="cuda")
+    k, lead = fused._cat._kargs()
+    if k == "sb6":
+        kk, (p0, p1, p2, b_), p3 = 0, lead, None
+    else:
+        kk, (p0, p1, p2, p3, b_) = 1, lead
+    _lib.call("rwkvq_gemm_dual_f16seg", kk, b_, p0, p1, p2, p3, 3 * C, C, C,
+              _lib.ptr(xs16), 6 * C, _lib.ptr(y1), _lib.X_F16, _lib.ptr(A),
+              4, ra, _lib.ptr(xs16[:, 2]), 6 * C, _lib.ptr(h1), modes, fl, T,
+              _lib.stream_handle())
+    y2 = torch.empty_like(y1)
+    fused.apply_into(xs16, y2, T, 6 * C, mode=_lib.X_F16)
+    h2 = torch.empty_like(h1)
+    _lib.call("rwkvq_gemm_f16_seg", _lib.ptr(A), 4, ra, C,
+              _lib.ptr(xs16[:, 2]), 6 * C, _lib.ptr(h2), T, modes, fl,
+              _lib.stream_handle())
+    assert torch.equal(y1, y2)
+    # fp16 outputs: the two launches' fp32 sums may round to adjacent halves
+    assert torch.allclose(h1.float(), h2.float(), rtol=2e-3, atol=2e-3)
