@@ -1008,10 +1008,19 @@ int rwkvq_gemm_dual_f16seg(int kind, int bits, const void* p0, const void* p1,
     st = one(fa, a);
     return st ? st : one(F_F16, b);
   }
+  // GEMM b's tiles take as long as a's at half the steps (fp16 weights are
+  // twice the bytes): split b's K in two where the workspace allows
   a.split = b.split = 1;
+  const SplitWs* ws = (flags_b & RWKVQ_NO_SPLIT) ? nullptr : current_ws();
+  if (ws && (in / kStepK) % 4 == 0 && tb <= ws->ncnt &&
+      tb * 2 * 128 * 128 * (long)sizeof(float) <= ws->bytes) {
+    b.split = 2;
+    b.ws = ws->ws;
+    b.cnt = ws->cnt;
+  }
   a.nt = rows / 128; b.nt = rows_b / 128;
   a.mt = b.mt = (int)mt;
-  const dim3 grid((unsigned)(ta + tb)), block(512);
+  const dim3 grid((unsigned)(ta + tb * b.split)), block(512);
   switch (fa) {
 #define RWKVQ_DUAL(F)                                                        \
   case F:                                                                    \
