@@ -279,6 +279,24 @@ int rwkvq_wkv7_scan_chunked(const float* r, long r_ld, const float* w,
                             int T, int H, int head_size, float* ws,
                             long ws_floats, void* stream);
 
+/* Prefill time-mix core from the projections: the per-channel inputs of
+ * rwkvq_wkv_prep (w, k' -> kp, v' -> vp, a, b; v_first written on layer 0,
+ * read otherwise) computed inside the chunk-operator kernel, then the
+ * chunked scan of rwkvq_wkv7_scan_chunked (r from rkv, v = v'); y, kp, vp
+ * are [B*T, H*64].  Equals rwkvq_wkv_prep + rwkvq_wkv7_scan_chunked with
+ * two launches instead of three and no w / a / b round trip through HBM.
+ * Replaces: the prep, the recurrence and its call site in the reference's
+ * prefill (quant_model.py:638-712, 118-125; rwkv7_ref.py:236-255). */
+int rwkvq_wkv7_prefill_chunked(const float* rkv, const float* yw,
+                               const float* ya, const float* yv,
+                               const float* w0, const float* a0,
+                               const float* v0, const float* k_k,
+                               const float* k_a, float* v_first, int layer0,
+                               float* kp, float* vp, const float* state_in,
+                               float* state_out, float* y, int B, int T,
+                               int H, int head_size, float* ws,
+                               long ws_floats, void* stream);
+
 /* Time-mix tail per head: out = ((GN(y) ln_w + ln_b) + (sum r k' r_k) v') g
  * with a two-pass group norm (eps 64e-5); r is rkv[:, 0, :].
  * Replaces: wkv_tail (reference: fused_tail.py:43-110) and the unfused

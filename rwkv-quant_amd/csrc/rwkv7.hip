@@ -674,11 +674,32 @@ __device__ __forceinline__ f32x4c_t mfma4(float a, float b, f32x4c_t c) {
 //   [5120, 6144)  Ryf[w][l][s] = Ry[16 w + 4 g + s][m]          s < 4
 //   [6144, 6400)  Yqf[l][s]    = Yq[4 g + s][m]                 s < 4
 // -- exactly the accumulator registers of the MFMAs that produce them.
+// Inputs of the prep step folded into the chunk-operator kernel (prefill:
+// rkvq_wkv7_prefill_chunked); unused by the plain chunked scan.
+struct PrepIn {
+  const float* rkv;          // [N, 3, D] r, k, v
+  const float* yw;
+  const float* ya;
+  const float* yv;           // null on layer 0
+  const float* w0;
+  const float* a0;
+  const float* v0;
+  const float* k_k;
+  const float* k_a;
+  float* vfirst;             // written on layer 0, read otherwise
+  int layer0;
+  float* kp;                 // out: k' [N, D]
+  float* vp;                 // out: v' [N, D]
+  int D;
+};
+
+template <bool PREP>
 __global__ void __launch_bounds__(256)
 wkv_chunk_ops_k(const float* __restrict__ r, long r_ld,
                 const float* __restrict__ w, const float* __restrict__ k,
                 const float* __restrict__ a, const float* __restrict__ b,
-                long ld, float* __restrict__ ops, int T, int H, int NC) {
+                long ld, float* __restrict__ ops, int T, int H, int NC,
+                PrepIn pi) {
   const int c = blockIdx.x % NC, bh = blockIdx.x / NC;
   const int h = bh % H, bi = bh / H;
   const int tid = threadIdx.x;
@@ -700,11 +721,36 @@ wkv_chunk_ops_k(const float* __restrict__ r, long r_ld,
     const int idx = tid + 256 * e, t = idx >> 6, kap = idx & 63;
     const int tg = c * kCL + t;
     float wvl = 1.f, kv = 0.f, av = 0.f, bv = 0.f, rv = 0.f;
-    if (tg < T) {
+    if (tg < T) {                       // (uniform: a wave is one step t)
       const size_t row = (size_t)bi * T + tg, col = (size_t)h * kHead + kap;
-      wvl = w[row * ld + col]; kv = k[row * ld + col];
-      av = a[row * ld + col]; bv = b[row * ld + col];
-      rv = r[row * r_ld + col];
+      if constexpr (PREP) {
+        // the per-channel inputs from r/k/v and the LoRA outputs, as
+        // wkv_prep_k; k' and v' also go out for the scan and the tail
+        const size_t e = row * pi.D + col;
+        const float kr = pi.rkv[(row * 3 + 1) * pi.D + col];
+        float vr = pi.rkv[(row * 3 + 2) * pi.D + col];
+        rv = pi.rkv[row * 3 * pi.D + col];
+        wvl = __expf(-0.606531f * sigm(pi.yw[e] + pi.w0[col]));
+        const float aw = sigm(pi.ya[e] + pi.a0[col]);
+        const float kkr = kr * pi.k_k[col];
+        const float ss = wave_sum_dpp(kkr * kkr);
+        const float kk = kkr / sqrtf(ss + 1e-12f);
+        kv = kr * (1.f + (aw - 1.f) * pi.k_a[col]);
+        av = -kk;
+        bv = kk * aw;
+        if (pi.layer0) {
+          pi.vfirst[e] = vr;
+        } else {
+          const float vf = pi.vfirst[e];
+          vr = vr + (vf - vr) * sigm(pi.yv[e] + pi.v0[col]);
+        }
+        pi.kp[e] = kv;
+        pi.vp[e] = vr;
+      } else {
+        wvl = w[row * ld + col]; kv = k[row * ld + col];
+        av = a[row * ld + col]; bv = b[row * ld + col];
+        rv = r[row * r_ld + col];
+      }
     }
     const float lw = fmaxf(logf(wvl), -60.f);
     sG[t + 1][kap] = lw;                 // summed in place below
@@ -1117,13 +1163,42 @@ int rwkvq_wkv7_scan_chunked(const float* r, long r_ld, const float* w,
   const int NC = ((T + kCL - 1) / kCL + 2) / 3 * 3;
   if (ws_floats < (long)B * H * NC * kOpsFloats || ((uintptr_t)ws & 15))
     return RWKVQ_ERR_ARG;
-  hipLaunchKernelGGL(wkv_chunk_ops_k, dim3(B * H * NC), dim3(256), 0,
+  hipLaunchKernelGGL(wkv_chunk_ops_k<false>, dim3(B * H * NC), dim3(256), 0,
                      (hipStream_t)stream, r, r_ld, w, k, a, b, ld, ws, T, H,
-                     NC);
+                     NC, PrepIn{});
   hipLaunchKernelGGL(wkv_chunk_scan_k, dim3(B * H * 4), dim3(256), 0,
                      (hipStream_t)stream, v, ld, ws,
                      state_in ? state_in : state_out, state_out, y, y_ld, T,
                      H, NC);
+  return ok_launch();
+}
+
+int rwkvq_wkv7_prefill_chunked(const float* rkv, const float* yw,
+                               const float* ya, const float* yv,
+                               const float* w0, const float* a0,
+                               const float* v0, const float* k_k,
+                               const float* k_a, float* v_first, int layer0,
+                               float* kp, float* vp, const float* state_in,
+                               float* state_out, float* y, int B, int T,
+                               int H, int head_size, float* ws,
+                               long ws_floats, void* stream) {
+  const int D = H * kHead;
+  if (B <= 0 || T <= 0 || H <= 0 || head_size != kHead || D % 256 || !rkv ||
+      !yw || !ya || !w0 || !a0 || !k_k || !k_a || !v_first || !kp || !vp ||
+      !y || !ws || !state_out || (!layer0 && (!yv || !v0)))
+    return RWKVQ_ERR_ARG;
+  const int NC = ((T + kCL - 1) / kCL + 2) / 3 * 3;
+  if (ws_floats < (long)B * H * NC * kOpsFloats || ((uintptr_t)ws & 15))
+    return RWKVQ_ERR_ARG;
+  const PrepIn pi{rkv, yw, ya, yv, w0, a0, v0, k_k, k_a, v_first, layer0, kp,
+                  vp, D};
+  hipLaunchKernelGGL(wkv_chunk_ops_k<true>, dim3(B * H * NC), dim3(256), 0,
+                     (hipStream_t)stream, nullptr, 0, nullptr, nullptr,
+                     nullptr, nullptr, 0, ws, T, H, NC, pi);
+  hipLaunchKernelGGL(wkv_chunk_scan_k, dim3(B * H * 4), dim3(256), 0,
+                     (hipStream_t)stream, vp, (long)D, ws,
+                     state_in ? state_in : state_out, state_out, y, (long)D,
+                     T, H, NC);
   return ok_launch();
 }
 

@@ -64,6 +64,9 @@ SIGNATURES = {
                         _I, _I, _I, _P],
     "rwkvq_wkv7_scan_chunked": [_P, _L, _P, _P, _P, _P, _P, _L, _P, _P, _P,
                                 _L, _I, _I, _I, _I, _P, _L, _P],
+    "rwkvq_wkv7_prefill_chunked": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                   _I, _P, _P, _P, _P, _P, _I, _I, _I, _I,
+                                   _P, _L, _P],
     "rwkvq_wkv_tail": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P],
     "rwkvq_wkv_tail_f16": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I,
                            _I, _P],

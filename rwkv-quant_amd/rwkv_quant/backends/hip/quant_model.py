@@ -51,6 +51,8 @@ WKV_CHUNK_MIN_T = 32           # sequence length from which the WKV scan
                                # runs in 16-step chunks (operators + a
                                # sequential pass on the matrix cores)
 WKV_CHUNK_OPS = 6400           # operator floats per (sequence, head, chunk)
+WKV_PREP_FUSED = True          # chunked prefill: per-channel prep inside the
+                               # chunk-operator kernel
 X16_PREFILL = True             # prefill GEMM inputs written as fp16 in the
                                # GEMM's pair order by their producers
 
@@ -668,6 +670,25 @@ class QuantRWKV7:
         """T > 1: per-channel inputs, the scan (step by step, or from
         WKV_CHUNK_MIN_T on in 16-step chunks), tail."""
         N, C, H = B * T, self.n_embd, self.n_head
+        if T >= WKV_CHUNK_MIN_T and WKV_PREP_FUSED:
+            # prep folded into the chunk operators: two launches
+            need = B * H * (-(-(-(-T // 16)) // 3) * 3) * WKV_CHUNK_OPS
+            ops = getattr(wk, "wkv_ops", None)
+            if ops is None or ops.numel() < need:
+                # allocated by the warm-up run that precedes any capture
+                ops = wk.wkv_ops = torch.empty(need, dtype=torch.float32,
+                                               device=self.device)
+            _lib.call("rwkvq_wkv7_prefill_chunked", _lib.ptr(wk.rkv),
+                      _lib.ptr(wk.yl["w"]), _lib.ptr(wk.yl["a"]),
+                      None if layer0 else _lib.ptr(wk.yl["v"]),
+                      _lib.ptr(tm.w0), _lib.ptr(tm.a0), _lib.ptr(tm.v0),
+                      _lib.ptr(tm.k_k), _lib.ptr(tm.k_a),
+                      _lib.ptr(wk.v_first), layer0, _lib.ptr(wk.kp),
+                      _lib.ptr(wk.vp), _lib.ptr(wkv_in), _lib.ptr(wkv_out),
+                      _lib.ptr(wk.y), B, T, H, self.head_size, _lib.ptr(ops),
+                      ops.numel(), st)
+            self._wkv_tail(tm, wk, N, C, st, o16)
+            return
         _lib.call("rwkvq_wkv_prep", _lib.ptr(wk.rkv), _lib.ptr(wk.yl["w"]),
                   _lib.ptr(wk.yl["a"]),
                   None if layer0 else _lib.ptr(wk.yl["v"]), _lib.ptr(tm.w0),
@@ -693,6 +714,11 @@ class QuantRWKV7:
                       _lib.ptr(wk.aa), _lib.ptr(wk.bb), C, _lib.ptr(wkv_in),
                       _lib.ptr(wkv_out), _lib.ptr(wk.y), C, B, T, H,
                       self.head_size, st)
+        self._wkv_tail(tm, wk, N, C, st, o16)
+
+    def _wkv_tail(self, tm, wk, N, C, st, o16):
+        """Group norm + bonus + gate into wk.o (fp32) or wk.o16 (fp16 in the
+        output projection's pair order o16)."""
         if o16 is not None:                 # fp16 in the o GEMM's order
             _lib.call("rwkvq_wkv_tail_f16", _lib.ptr(wk.y), _lib.ptr(wk.rkv),
                       _lib.ptr(wk.kp), _lib.ptr(wk.vp), _lib.ptr(wk.yl["g"]),

@@ -288,3 +288,46 @@ def test_graph_prefill_equals_eager(toy):
         for a, b in zip(st, st_ref):
             for x, y in zip(a, b):
                 assert torch.equal(x, y)
+
+
+@pytest.mark.parametrize("layer0", [1, 0])
+@pytest.mark.parametrize("T", [37, 160])
+def test_prefill_core_fused_equals_prep_then_chunked(layer0, T):
+    """rwkvq_wkv7_prefill_chunked (prep folded into the chunk operators) ==
+    rwkvq_wkv_prep + rwkvq_wkv7_scan_chunked: y, state, k', v' and v_first
+    to 1e-6 relative (the two kernels may contract the prep arithmetic
+    differently)."""
+    g = torch.Generator().manual_seed(T + layer0)
+    B, H = 2, 4
+    D, N = H * 64, 2 * T
+    t = lambda *s, sc=1.0: (torch.randn(*s, generator=g) * sc).cuda()
+    rkv, yw, ya, yv = t(N, 3 * D), t(N, D), t(N, D), t(N, D)
+    w0, a0, v0 = t(D, sc=0.5), t(D), t(D)
+    k_k, k_a = t(D).abs(), t(D).abs()
+    vf0 = t(N, D)
+    st0 = t(B, H, 64, 64, sc=0.1)
+    P, s = _lib.ptr, _lib.stream_handle()
+    nc = ((-(-T // 16)) + 2) // 3 * 3
+    ops = torch.empty(B * H * nc * 6400, device="cuda")
+    # reference: prep, then the chunked scan
+    w, kp, vp, aa, bb = (torch.empty(N, D, device="cuda") for _ in range(5))
+    vf1 = vf0.clone()
+    _lib.call("rwkvq_wkv_prep", P(rkv), P(yw), P(ya), None if layer0 else
+              P(yv), P(w0), P(a0), None if layer0 else P(v0), P(k_k), P(k_a),
+              P(vf1), layer0, P(w), P(kp), P(vp), P(aa), P(bb), N, D, 64, s)
+    st1, y1 = torch.empty_like(st0), torch.empty(N, D, device="cuda")
+    _lib.call("rwkvq_wkv7_scan_chunked", P(rkv), 3 * D, P(w), P(kp), P(vp),
+              P(aa), P(bb), D, P(st0), P(st1), P(y1), D, B, T, H, 64, P(ops),
+              ops.numel(), s)
+    # fused
+    vf2 = vf0.clone()
+    kp2, vp2 = torch.empty_like(kp), torch.empty_like(vp)
+    st2, y2 = torch.empty_like(st0), torch.empty(N, D, device="cuda")
+    _lib.call("rwkvq_wkv7_prefill_chunked", P(rkv), P(yw), P(ya),
+              None if layer0 else P(yv), P(w0), P(a0),
+              None if layer0 else P(v0), P(k_k), P(k_a), P(vf2), layer0,
+              P(kp2), P(vp2), P(st0), P(st2), P(y2), B, T, H, 64, P(ops),
+              ops.numel(), s)
+    rel = lambda a, b: float((a - b).abs().max() / b.abs().max())
+    for a_, b_ in ((y2, y1), (st2, st1), (kp2, kp), (vp2, vp), (vf2, vf1)):
+        assert rel(a_, b_) < 1e-6
