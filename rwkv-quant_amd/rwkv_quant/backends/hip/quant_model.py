@@ -271,6 +271,9 @@ class QuantTMix:
                           [wk.yl[b] for b in branches],
                           [_lib.EPI_STORE] * len(branches), N)
             return
+        if x16_order is None and N < GEMM_MIN_BATCH_NB:
+            self._run_lora_batch(wk)
+            return
         # prefill: the MFMA GEMM over the dense fp16 factors; one launch for
         # the down products of all branches (their lerp slots v, w, a, g are
         # adjacent in wk.xs), one per up product
@@ -290,6 +293,35 @@ class QuantTMix:
         # the down GEMM wrote rows of `tot` values, branch j from column
         # sum(rps[:j]) on
         self._run_ups(wk, x16, order, rps, B_pad)
+
+    def _run_lora_batch(self, wk):
+        """Decode batches of 9..127 rows: the down products as the
+        segmented matrix-core GEMV in 16-row launches (the padded stacked
+        factors; a GEMM would have a handful of output tiles here), into
+        per-branch padded buffers carved from wk.h_cat, then the up products
+        in one grouped launch."""
+        N, C = wk.N, self.C
+        order, rps, A_cat, B_pad, modes = self._prefill_mats()
+        nseg = len(order)
+        hp = [wk.h_cat.view(-1)[N * sum(rps[:j]):N * sum(rps[:j + 1])]
+              .view(N, rps[j]) for j in range(nseg)]
+        xs_flat = wk.xs.view(N, 6 * C)
+        x0 = xs_flat[:, self.SLOT[order[0]] * C:]
+        rows = (ctypes.c_int * nseg)(*rps)
+        for n0 in range(0, N, 16):
+            n = min(16, N - n0)
+            ys = (ctypes.c_void_p * nseg)(*[h[n0:].data_ptr() for h in hp])
+            _lib.call("rwkvq_gemv_f16_seg", _lib.ptr(A_cat), nseg, rows, C,
+                      _lib.ptr(x0[n0:]), 6 * C, ys, n, modes, _stream())
+        P = ctypes.c_void_p
+        _lib.call("rwkvq_gemm_f16_grouped", nseg,
+                  (P * nseg)(*[B_pad[b].data_ptr() for b in order]),
+                  (ctypes.c_int * nseg)(*[C] * nseg),
+                  (ctypes.c_int * nseg)(*rps),
+                  (P * nseg)(*[h.data_ptr() for h in hp]),
+                  (ctypes.c_long * nseg)(*rps),
+                  (P * nseg)(*[wk.yl[b].data_ptr() for b in order]),
+                  N, 0, 0, _stream())
 
     def run_rkv_lora_x16(self, wk, x_order):
         """Prefill with fp16 lerp outputs (pair order x_order): the r/k/v
