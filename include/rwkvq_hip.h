@@ -387,7 +387,7 @@ int rwkvq_gemm_f16_grouped(int nseg, const uint16_t* const* w,
                            void* stream);
 
 /* Dense fp16 rows in up to 8 segments of one matrix w [sum rows, in], for
- * 1..16 input rows, on the matrix cores: segment j (rows seg_rows[j], a
+ * 1..32 input rows, on the matrix cores: segment j (rows seg_rows[j], a
  * multiple of 16) reads x[n * x_ld + j * in + c] and writes
  * seg_y[j][n * seg_rows[j] + r] = epi_j(sum_c x . w), epi_j = 4-bit field
  * j of seg_modes (RWKVQ_EPI_*).  in % 128 == 0.

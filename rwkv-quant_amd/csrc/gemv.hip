@@ -34,6 +34,10 @@ using namespace rwkvq;
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
+#ifndef RWKVQ_BG_NB2
+#define RWKVQ_BG_NB2 1
+#endif
+
 namespace {
 
 struct GemvArgs {
@@ -290,7 +294,9 @@ gemv_kernel(GemvArgs a) {
 // meet in LDS in a fixed order (deterministic); each output element
 // depends only on its own input row, so a row's result does not depend on
 // the other rows of the batch.
-template <int FMT, int RT, int NS, int KSMAX>
+// NB blocks of 16 input rows share each decoded weight fragment (NB = 2:
+// batches of 17..32 rows in one pass over the weights).
+template <int FMT, int RT, int NS, int KSMAX, int NB = 1>
 __global__ void __launch_bounds__(64 * KSMAX)
 bgemv_kernel(GemvArgs a) {
   using RawT = typename RawOf<FMT>::T;
@@ -315,9 +321,14 @@ bgemv_kernel(GemvArgs a) {
     }
   }
   const int gw = wave * a.rpw * 4;         // first group of the wave's slice
-  const bool xon = i < a.n;
-  const float* xr = a.x + (size_t)(xon ? i : 0) * a.x_ld +
-                    (size_t)seg * a.in + q * 32;
+  bool xon[NB];
+  const float* xr[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    xon[b] = i + 16 * b < a.n;
+    xr[b] = a.x + (size_t)(xon[b] ? i + 16 * b : 0) * a.x_ld +
+            (size_t)seg * a.in + q * 32;
+  }
 
   auto load_w = [&](int g, RawT (&dst)[RT]) {
 #pragma unroll
@@ -327,44 +338,56 @@ bgemv_kernel(GemvArgs a) {
   // unconditional loads (lanes past the batch read input row 0 and zero
   // their B operand later): no branches, so the compiler's load counting
   // stays exact and a wait covers only the step it feeds
-  auto load_x = [&](int g0, float4 (&dst)[8]) {
-    const float4* p = reinterpret_cast<const float4*>(xr + (size_t)g0 * 32);
+  auto load_x = [&](int g0, float4 (&dst)[NB][8]) {
 #pragma unroll
-    for (int t = 0; t < 8; ++t) dst[t] = p[t];
+    for (int b = 0; b < NB; ++b) {
+      const float4* p =
+          reinterpret_cast<const float4*>(xr[b] + (size_t)g0 * 32);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) dst[b][t] = p[t];
+    }
   };
 
-  f32x4_t acc[RT];
+  f32x4_t acc[NB][RT];
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt) acc[rt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) acc[b][rt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  auto mma_step = [&](int st, RawT (&w_raw)[RT], float4 (&xv)[8]) {
-    half8_t bx[4];
+  auto mma_step = [&](int st, RawT (&w_raw)[RT], float4 (&xv)[NB][8]) {
+    half8_t bx[NB][4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      int ca, cb;
-      step_cols<FMT>(j, ca, cb);
-      uint4 xp = x_pairs<FMT>(xv[ca >> 2], xv[cb >> 2]);
-      if (!xon) xp = make_uint4(0u, 0u, 0u, 0u);
-      bx[j] = __builtin_bit_cast(half8_t, xp);
-    }
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        int ca, cb;
+        step_cols<FMT>(j, ca, cb);
+        uint4 xp = x_pairs<FMT>(xv[b][ca >> 2], xv[b][cb >> 2]);
+        if (!xon[b]) xp = make_uint4(0u, 0u, 0u, 0u);
+        bx[b][j] = __builtin_bit_cast(half8_t, xp);
+      }
     const int kb = (gw + 4 * st + q) & 7;   // group within its superblock
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
       uint32_t w[16];
       dequant_group<FMT>(w_raw[rt], kb, w);
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-            __builtin_bit_cast(half8_t, make_uint4(w[4 * j], w[4 * j + 1],
-                                                   w[4 * j + 2], w[4 * j + 3])),
-            bx[j], acc[rt], 0, 0, 0);
+      for (int j = 0; j < 4; ++j) {
+        const half8_t av = __builtin_bit_cast(
+            half8_t,
+            make_uint4(w[4 * j], w[4 * j + 1], w[4 * j + 2], w[4 * j + 3]));
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+          acc[b][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+              av, bx[b][j], acc[b][rt], 0, 0, 0);
+      }
     }
   };
 
   if (NS == 2) {
     // both steps' loads in flight at once
     RawT wa[RT], wb[RT];
-    float4 xa[8], xb[8];
+    float4 xa[NB][8], xb[NB][8];
     load_w(gw + q, wa);
     load_x(gw, xa);
     load_w(gw + 4 + q, wb);
@@ -379,7 +402,7 @@ bgemv_kernel(GemvArgs a) {
     // straight-line: step s + 1 loads while step s multiplies, in two
     // register sets (compile-time indices, no copies)
     RawT w2[2][RT];
-    float4 x2[2][8];
+    float4 x2[2][NB][8];
     load_w(gw + q, w2[0]);
     load_x(gw, x2[0]);
 #pragma unroll
@@ -396,7 +419,7 @@ bgemv_kernel(GemvArgs a) {
     // any step count: the same two register sets in a loop.  Loads past
     // the slice's last step are clamped to it (L2 hits, never used).
     RawT wa[RT], wb[RT];
-    float4 xa[8], xb[8];
+    float4 xa[NB][8], xb[NB][8];
     const int last = a.rpw - 1;
     load_w(gw + q, wa);
     load_x(gw, xa);
@@ -415,13 +438,15 @@ bgemv_kernel(GemvArgs a) {
     }
   }
 
-  // ---- K slices meet in LDS: red[wave][rt][v][lane]
-  __shared__ float red[KSMAX * RT * 256];
+  // ---- K slices meet in LDS: red[wave][b][rt][v][lane]
+  __shared__ float red[KSMAX * NB * RT * 256];
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt)
+  for (int b = 0; b < NB; ++b)
 #pragma unroll
-    for (int v = 0; v < 4; ++v)
-      red[(wave * RT + rt) * 256 + v * 64 + lane] = acc[rt][v];
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        red[((wave * NB + b) * RT + rt) * 256 + v * 64 + lane] = acc[b][rt][v];
   __syncthreads();
   constexpr int kRows = 16 * RT;
   const int mode = a.mode == RWKVQ_EPI_PER_SEG ? (a.seg_modes >> (4 * seg)) & 15
@@ -432,12 +457,13 @@ bgemv_kernel(GemvArgs a) {
     for (int j = 0; j < 8; ++j)
       seg_hi = j == seg ? a.seg_end[j] : seg_hi;
   }
-  for (int idx = threadIdx.x; idx < kRows * 16; idx += a.ks * 64) {
+  for (int idx = threadIdx.x; idx < kRows * 16 * NB; idx += a.ks * 64) {
     const int n = idx / kRows, r = idx % kRows;   // rows fastest: coalesced
     if (n >= a.n) break;
-    const int e = (r >> 4) * 256 + (r & 3) * 64 + n + 16 * ((r & 15) >> 2);
+    const int e = ((n >> 4) * RT + (r >> 4)) * 256 + (r & 3) * 64 + (n & 15) +
+                  16 * ((r & 15) >> 2);
     float v = 0.f;
-    for (int k = 0; k < a.ks; ++k) v += red[k * RT * 256 + e];
+    for (int k = 0; k < a.ks; ++k) v += red[k * NB * RT * 256 + e];
     const int row = row0 + r;
     if (FMT == F_RTN8) v *= f16_bits_to_f32(a.d[row]);
     float* yp = a.nseg_tab > 0
@@ -454,20 +480,20 @@ bgemv_kernel(GemvArgs a) {
   }
 }
 
-template <int FMT, int RT, int KSMAX>
+template <int FMT, int RT, int KSMAX, int NB = 1>
 int launch_bg_rt(GemvArgs a, hipStream_t s) {
   dim3 grid(a.rows / (16 * RT)), block(64 * a.ks);
-  for (int n0 = 0; n0 < a.n; n0 += 16) {
+  for (int n0 = 0; n0 < a.n; n0 += 16 * NB) {
     GemvArgs b = a;
     b.x = a.x + (size_t)n0 * a.x_ld;
     b.y = a.y + (size_t)n0 * a.rows;
-    b.n = a.n - n0 < 16 ? a.n - n0 : 16;
+    b.n = a.n - n0 < 16 * NB ? a.n - n0 : 16 * NB;
     if (a.rpw == 2)
-      hipLaunchKernelGGL((bgemv_kernel<FMT, RT, 2, KSMAX>), grid, block, 0, s, b);
+      hipLaunchKernelGGL((bgemv_kernel<FMT, RT, 2, KSMAX, NB>), grid, block, 0, s, b);
     else if (a.rpw == 4)
-      hipLaunchKernelGGL((bgemv_kernel<FMT, RT, 4, KSMAX>), grid, block, 0, s, b);
+      hipLaunchKernelGGL((bgemv_kernel<FMT, RT, 4, KSMAX, NB>), grid, block, 0, s, b);
     else
-      hipLaunchKernelGGL((bgemv_kernel<FMT, RT, 0, KSMAX>), grid, block, 0, s, b);
+      hipLaunchKernelGGL((bgemv_kernel<FMT, RT, 0, KSMAX, NB>), grid, block, 0, s, b);
   }
   return hipGetLastError() == hipSuccess ? RWKVQ_OK : RWKVQ_ERR_LAUNCH;
 }
@@ -488,6 +514,17 @@ int launch_bg(GemvArgs a, hipStream_t s) {
   } else {
     ks = 8;
     while (steps % ks) --ks;
+  }
+  if (RWKVQ_BG_NB2 && a.n > 16) {
+    // 17+ rows: two 16-row blocks per pass (each decoded weight feeds both;
+    // the second block's x doubles the registers, so at most 8 K slices)
+    ks = 8;
+    while (steps % ks) --ks;
+    a.ks = ks;
+    a.rpw = steps / ks;
+    if (a.out_per % 32 == 0 && a.rows / 32 >= 256)
+      return launch_bg_rt<FMT, 2, 8, 2>(a, s);
+    return launch_bg_rt<FMT, 1, 8, 2>(a, s);
   }
   a.ks = ks;
   a.rpw = steps / ks;
@@ -636,8 +673,9 @@ int rwkvq_gemv_f16_seg(const uint16_t* w, int nseg, const int* seg_rows,
                        int in, const float* x, long x_ld,
                        float* const* seg_y, int n, int seg_modes,
                        void* stream) {
+  // one launch covers the batch: 16 rows, or 32 with the two-block kernel
   if (!w || !x || nseg < 1 || nseg > 8 || in <= 0 || in % 128 || n < 1 ||
-      n > 16)
+      n > (RWKVQ_BG_NB2 ? 32 : 16))
     return RWKVQ_ERR_ARG;
   GemvArgs a{};
   int rows = 0;

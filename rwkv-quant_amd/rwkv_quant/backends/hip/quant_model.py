@@ -55,6 +55,7 @@ WKV_PREP_FUSED = True          # chunked prefill: per-channel prep inside the
                                # chunk-operator kernel
 X16_PREFILL = True             # prefill GEMM inputs written as fp16 in the
                                # GEMM's pair order by their producers
+LORA_GEMV_ROWS = 32            # decode-batch rows per LoRA-down GEMV launch
 
 _LORA = ("w1", "w2", "a1", "a2", "v1", "v2", "g1", "g2")
 
@@ -296,7 +297,7 @@ class QuantTMix:
 
     def _run_lora_batch(self, wk):
         """Decode batches of 9..127 rows: the down products as the
-        segmented matrix-core GEMV in 16-row launches (the padded stacked
+        segmented matrix-core GEMV in 32-row launches (the padded stacked
         factors; a GEMM would have a handful of output tiles here), into
         per-branch padded buffers carved from wk.h_cat, then the up products
         in one grouped launch."""
@@ -308,8 +309,8 @@ class QuantTMix:
         xs_flat = wk.xs.view(N, 6 * C)
         x0 = xs_flat[:, self.SLOT[order[0]] * C:]
         rows = (ctypes.c_int * nseg)(*rps)
-        for n0 in range(0, N, 16):
-            n = min(16, N - n0)
+        for n0 in range(0, N, LORA_GEMV_ROWS):
+            n = min(LORA_GEMV_ROWS, N - n0)
             ys = (ctypes.c_void_p * nseg)(*[h[n0:].data_ptr() for h in hp])
             _lib.call("rwkvq_gemv_f16_seg", _lib.ptr(A_cat), nseg, rows, C,
                       _lib.ptr(x0[n0:]), 6 * C, ys, n, modes, _stream())

@@ -163,7 +163,7 @@ def test_gemm_f16_per_segment_epilogue():
                               atol=1e-5)
 
 
-@pytest.mark.parametrize("n", [1, 3, 8, 16])
+@pytest.mark.parametrize("n", [1, 3, 8, 16, 17, 32])
 @pytest.mark.parametrize("ranks", [(64, 96, 96, 256), (96, 96, 256)])
 def test_gemv_f16_segments(n, ranks):
     """The decode LoRA down products in one launch: segment j of the
@@ -195,11 +195,11 @@ def test_gemv_f16_segments(n, ranks):
 
 def test_gemv_f16_segments_errors():
     A = torch.zeros(96, 2048, dtype=torch.float16, device="cuda")
-    x = torch.zeros(17, 2048, device="cuda")
-    y = torch.empty(17, 96, device="cuda")
+    x = torch.zeros(33, 2048, device="cuda")
+    y = torch.empty(33, 96, device="cuda")
     import ctypes
     yp = (ctypes.c_void_p * 1)(y.data_ptr())
-    for rows, n in ((90, 4), (96, 17), (96, 0)):
+    for rows, n in ((90, 4), (96, 33), (96, 0)):
         r = (ctypes.c_int * 1)(rows)
         with pytest.raises(_lib.HipKernelError):
             _lib.call("rwkvq_gemv_f16_seg", _lib.ptr(A), 1, r, 2048,

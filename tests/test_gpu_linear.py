@@ -80,7 +80,7 @@ def test_dequant_asym_bit_exact():
 @pytest.mark.parametrize("kind,bits", FORMATS)
 @pytest.mark.parametrize("shape", [(2048, 2048), (8192, 2048), (2048, 8192),
                                    (512, 2560), (256, 10240), (96, 6144)])
-@pytest.mark.parametrize("n", [1, 2, 3, 8, 20])
+@pytest.mark.parametrize("n", [1, 2, 3, 8, 20, 40])
 def test_gemv_relmax(kind, bits, shape, n):
     print(f"gemv {kind}@{bits} {shape} n={n}", flush=True)
     w = _w(*shape, seed=shape[0] + bits, outliers=2)
