@@ -15,8 +15,10 @@ Same contract as the reference Metal classes
                                matrices in one launch
 
 Batches of up to GEMM_MIN_BATCH_NB - 1 rows take the GEMV kernel (which
-reads each weight once per 8 rows); larger batches (prefill) take the MFMA
-GEMM with the dequantization fused into its operand load.  Every path runs a HIP kernel of librwkvq_hip; nothing here computes
+reads each weight once per 16 or 32 rows), except from GEMM_MID_BATCH rows
+on (and from GEMM_WIDE_BATCH rows for outputs of GEMM_WIDE_ROWS rows or
+more) where the MFMA GEMM is the faster one; larger batches (prefill) take
+the MFMA GEMM with the dequantization fused into its operand load.  Every path runs a HIP kernel of librwkvq_hip; nothing here computes
 on the CPU.
 """
 import numpy as np
@@ -27,6 +29,13 @@ from .repack import rtn8_device, sb6_device, sym_device
 
 GEMM_MIN_BATCH_NB = 128          # reference: quant_linear_gw.py:153
 GEMM_ROW_TILE = 128              # output rows per MFMA GEMM tile
+# Below GEMM_MIN_BATCH_NB the batched GEMV re-reads x once per 16..32 output
+# rows; measured on MI355X (2.9B shapes), the MFMA GEMM (x staged once per
+# 128 rows) is faster from 33 rows on every shape, and from 17 rows where
+# the output has at least GEMM_WIDE_ROWS rows (enough 128-row tiles).
+GEMM_MID_BATCH = 33
+GEMM_WIDE_BATCH = 17
+GEMM_WIDE_ROWS = 4096
 
 
 def _np(t):
@@ -80,7 +89,11 @@ class _HipLinearBase:
     def _apply(self, x2, y, out_per=None, mode=_lib.EPI_STORE, n=None,
                x_ld=0):
         rows = n if n is not None else x2.shape[0]
-        if rows < GEMM_MIN_BATCH_NB:
+        if rows < GEMM_MIN_BATCH_NB and self.gemm_ok(out_per) and (
+                rows >= GEMM_MID_BATCH or (rows >= GEMM_WIDE_BATCH and
+                                           self.out_features >= GEMM_WIDE_ROWS)):
+            self._run("gemm", x2, y, out_per, mode, n, x_ld)
+        elif rows < GEMM_MIN_BATCH_NB:
             self._gemv(x2, y, out_per, mode, n, x_ld)
         elif self.gemm_ok(out_per):
             self._run("gemm", x2, y, out_per, mode, n, x_ld)
