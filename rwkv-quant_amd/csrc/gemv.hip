@@ -50,6 +50,7 @@ struct GemvArgs {
   float* y;              // [N, rows]
   long x_ld;
   int rows, in, out_per, n_seg, ks, rg, rpw, mode, n;
+  int ilv;               // lane-dot kernel: interleaved row order (see there)
   // segment table (matrix-core kernel, rwkvq_gemv_f16_seg): segment j
   // holds rows [seg_end[j-1], seg_end[j]), reads x at x + j * in and writes
   // seg_y[j] [n, rows of j]; 0 segments = uniform out_per segments
@@ -128,12 +129,22 @@ gemv_kernel(GemvArgs a) {
   // rows after them belong to another wave, possibly on another XCD, and
   // reading them there costs a second HBM fetch
   const int last = max(min(row_base + a.rpw, a.rows) - 1, 0);
+  // interleaved order (one segment, grid covering the rows exactly): batch
+  // b of row-wave w holds rows b * bstride + w * RS + j, so that at any
+  // moment the grid's waves stream one contiguous stretch of the matrix
+  // instead of points a whole wave's share (rpw rows) apart
+  const int wrow = blockIdx.x * a.rg + rgi;
+  const int bstride = gridDim.x * a.rg * RS;
+  auto row_of = [&](int r) {
+    return a.ilv ? (r / RS) * bstride + wrow * RS + r % RS : row_base + r;
+  };
   Raw cur[RS], nxt[RS];
 #pragma unroll
   for (int j = 0; j < RS; ++j)
-    load_raw<FMT>(a, min(row_base + j, last), ng, nsb, gl, cur[j]);
+    load_raw<FMT>(a, a.ilv ? row_of(j) : min(row_base + j, last), ng, nsb,
+                  gl, cur[j]);
 
-  const int seg = wg_row0 < a.rows ? wg_row0 / a.out_per : 0;
+  const int seg = !a.ilv && wg_row0 < a.rows ? wg_row0 / a.out_per : 0;
   for (int item = threadIdx.x; item < NN * ng; item += blockDim.x) {
     const int n = item / ng, gg = item % ng;
     if (n < a.n) {
@@ -173,7 +184,10 @@ gemv_kernel(GemvArgs a) {
     // prefetch the next batch before touching this one
 #pragma unroll
     for (int j = 0; j < RS; ++j)
-      load_raw<FMT>(a, min(row_base + r0 + RS + j, last), ng, nsb, gl, nxt[j]);
+      load_raw<FMT>(a,
+                    !a.ilv ? min(row_base + r0 + RS + j, last)
+                    : r0 + RS < a.rpw ? row_of(r0 + RS + j) : row_of(a.rpw - 1),
+                    ng, nsb, gl, nxt[j]);
 
     float acc[NN][RS];
 #pragma unroll
@@ -250,7 +264,7 @@ gemv_kernel(GemvArgs a) {
       for (int n = 0; n < NN; ++n)
 #pragma unroll
         for (int j = 0; j < RS; ++j) {
-          const int row = row_base + r0 + j;
+          const int row = row_of(r0 + j);
           if (lane != n * RS + j || n >= a.n || r0 + j >= nrows) continue;
           float v = acc[n][j];
           if (FMT == F_RTN8) v *= f16_bits_to_f32(a.d[row]);
@@ -542,6 +556,9 @@ int launch_bg(GemvArgs a, hipStream_t s) {
 #ifndef RWKVQ_TARGET_WAVES
 #define RWKVQ_TARGET_WAVES 4096
 #endif
+#ifndef RWKVQ_GEMV_ILV
+#define RWKVQ_GEMV_ILV 1
+#endif
 #ifndef RWKVQ_MAX_RPW
 #define RWKVQ_MAX_RPW 32
 #endif
@@ -564,6 +581,11 @@ int launch_rs(GemvArgs a, hipStream_t s) {
   const int rows_per_wg = a.rg * rpw;
   dim3 grid((a.rows + rows_per_wg - 1) / rows_per_wg);
   dim3 block(64 * a.ks * a.rg);
+  // interleaved row order for large one-segment matrices only (the heads:
+  // 28.4 vs 29.6 us for 2048->65536 int8); below 16384 row-slices it was
+  // slower (measured)
+  a.ilv = RWKVQ_GEMV_ILV && a.n_seg == 1 && rows_waves > 16384 &&
+          (long)grid.x * rows_per_wg == (long)a.rows;
   const int ng = a.in / 32;
   // up to 8 input rows per launch (each weight read once per chunk); the
   // staged x must fit the LDS budget of 96 KiB per workgroup

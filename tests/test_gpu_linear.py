@@ -96,6 +96,16 @@ def test_gemv_relmax(kind, bits, shape, n):
         assert relmax(y, _operand_ref(kind, lin, qt, x)) < 2e-5
 
 
+@pytest.mark.parametrize("kind,bits", FORMATS)
+@pytest.mark.parametrize("shape", [(20480, 2048), (4096, 10240)])
+@pytest.mark.parametrize("n", [1, 2])
+def test_gemv_relmax_interleaved_rows(kind, bits, shape, n):
+    """Beyond 16384 row-slices the lane-dot kernel takes the interleaved
+    row order (a wave's row batches one grid-stride apart), with one K
+    slice per wave (20480 rows) and five (K = 10240)."""
+    test_gemv_relmax(kind, bits, shape, n)
+
+
 def _operand_ref(kind, lin, qt, x):
     """float64 product of the fp16 operands of the matrix-core path."""
     x16 = x.half().double().numpy()
