@@ -50,7 +50,6 @@ struct GemvArgs {
   float* y;              // [N, rows]
   long x_ld;
   int rows, in, out_per, n_seg, ks, rg, rpw, mode, n;
-  int ilv;               // lane-dot kernel: interleaved row order (see there)
   // segment table (matrix-core kernel, rwkvq_gemv_f16_seg): segment j
   // holds rows [seg_end[j-1], seg_end[j]), reads x at x + j * in and writes
   // seg_y[j] [n, rows of j]; 0 segments = uniform out_per segments
@@ -95,7 +94,12 @@ __device__ __forceinline__ void x_group(const float* __restrict__ xp,
   sums[2] = sf;
 }
 
-template <int FMT, int NN, int RS>
+// ILV: interleaved row order (the heads); otherwise blocked rows.  The
+// sb6 codes of blocked rows are read with non-temporal loads (1.5B
+// COMPRESSION decode B = 1 1.213 -> 1.169 ms); for the sym / rtn formats,
+// the heads and the batched kernel they were slower (measured).
+template <int FMT, int NN, int RS, bool ILV = false,
+          bool NT = !ILV && FMT <= F_SB6_6>
 __global__ void __launch_bounds__(512)
 gemv_kernel(GemvArgs a) {
   const int lane = threadIdx.x & 63;
@@ -136,15 +140,15 @@ gemv_kernel(GemvArgs a) {
   const int wrow = blockIdx.x * a.rg + rgi;
   const int bstride = gridDim.x * a.rg * RS;
   auto row_of = [&](int r) {
-    return a.ilv ? (r / RS) * bstride + wrow * RS + r % RS : row_base + r;
+    return ILV ? (r / RS) * bstride + wrow * RS + r % RS : row_base + r;
   };
   Raw cur[RS], nxt[RS];
 #pragma unroll
   for (int j = 0; j < RS; ++j)
-    load_raw<FMT>(a, a.ilv ? row_of(j) : min(row_base + j, last), ng, nsb,
-                  gl, cur[j]);
+    load_raw<FMT, NT>(a, ILV ? row_of(j) : min(row_base + j, last), ng,
+                        nsb, gl, cur[j]);
 
-  const int seg = !a.ilv && wg_row0 < a.rows ? wg_row0 / a.out_per : 0;
+  const int seg = !ILV && wg_row0 < a.rows ? wg_row0 / a.out_per : 0;
   for (int item = threadIdx.x; item < NN * ng; item += blockDim.x) {
     const int n = item / ng, gg = item % ng;
     if (n < a.n) {
@@ -184,8 +188,8 @@ gemv_kernel(GemvArgs a) {
     // prefetch the next batch before touching this one
 #pragma unroll
     for (int j = 0; j < RS; ++j)
-      load_raw<FMT>(a,
-                    !a.ilv ? min(row_base + r0 + RS + j, last)
+      load_raw<FMT, NT>(a,
+                    !ILV ? min(row_base + r0 + RS + j, last)
                     : r0 + RS < a.rpw ? row_of(r0 + RS + j) : row_of(a.rpw - 1),
                     ng, nsb, gl, nxt[j]);
 
@@ -347,7 +351,7 @@ bgemv_kernel(GemvArgs a) {
   auto load_w = [&](int g, RawT (&dst)[RT]) {
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
-      load_raw<FMT>(a, row0 + 16 * rt + i, ng, nsb, g, dst[rt]);
+      load_raw<FMT, false>(a, row0 + 16 * rt + i, ng, nsb, g, dst[rt]);
   };
   // unconditional loads (lanes past the batch read input row 0 and zero
   // their B operand later): no branches, so the compiler's load counting
@@ -584,8 +588,10 @@ int launch_rs(GemvArgs a, hipStream_t s) {
   // interleaved row order for large one-segment matrices only (the heads:
   // 28.4 vs 29.6 us for 2048->65536 int8); below 16384 row-slices it was
   // slower (measured)
-  a.ilv = RWKVQ_GEMV_ILV && a.n_seg == 1 && rows_waves > 16384 &&
-          (long)grid.x * rows_per_wg == (long)a.rows;
+  // (4-row batches, one or two input rows)
+  const bool ilv = RWKVQ_GEMV_ILV && RS == 4 && a.n <= 2 && a.n_seg == 1 &&
+                   rows_waves > 16384 &&
+                   (long)grid.x * rows_per_wg == (long)a.rows;
   const int ng = a.in / 32;
   // up to 8 input rows per launch (each weight read once per chunk); the
   // staged x must fit the LDS budget of 96 KiB per workgroup
@@ -599,8 +605,18 @@ int launch_rs(GemvArgs a, hipStream_t s) {
     const int nn = b.n <= 1 ? 1 : b.n <= 2 ? 2 : b.n <= 4 ? 4 : 8;
     const size_t lds = (size_t)nn * ng * (16 + 3) * 4;
     switch (nn) {
-      case 1: hipLaunchKernelGGL((gemv_kernel<FMT, 1, RS>), grid, block, lds, s, b); break;
-      case 2: hipLaunchKernelGGL((gemv_kernel<FMT, 2, RS>), grid, block, lds, s, b); break;
+      case 1:
+        if (ilv)
+          hipLaunchKernelGGL((gemv_kernel<FMT, 1, RS, RS == 4>), grid, block, lds, s, b);
+        else
+          hipLaunchKernelGGL((gemv_kernel<FMT, 1, RS>), grid, block, lds, s, b);
+        break;
+      case 2:
+        if (ilv)
+          hipLaunchKernelGGL((gemv_kernel<FMT, 2, RS, RS == 4>), grid, block, lds, s, b);
+        else
+          hipLaunchKernelGGL((gemv_kernel<FMT, 2, RS>), grid, block, lds, s, b);
+        break;
       case 4: hipLaunchKernelGGL((gemv_kernel<FMT, 4, RS>), grid, block, lds, s, b); break;
       default:
         if constexpr (RS == 2)   // 8 columns x 4 rows would spill VGPRs

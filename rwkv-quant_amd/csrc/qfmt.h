@@ -45,19 +45,19 @@ struct Raw {
   // consumer's wait is for its own loads, not for the whole batch
 };
 
-template <int FMT, class Args>
+template <int FMT, bool NT = true, class Args>
 __device__ __forceinline__ void load_raw(const Args& a, int row, int ng,
                                          int nsb, int g, Raw& r) {
   if (FMT == F_SYM8 || FMT == F_RTN8) {
     const uint8_t* p = a.q + (size_t)row * a.in;     // wave-uniform
-    r.a = ld16(p + g * 32);
-    r.b = ld16(p + g * 32 + 16);
+    r.a = ld16_w<NT>(p + g * 32);
+    r.b = ld16_w<NT>(p + g * 32 + 16);
   } else {
     const uint8_t* p = a.q + (size_t)row * ng * 16;  // wave-uniform
-    r.a = ld16(p + g * 16);
+    r.a = ld16_w<NT>(p + g * 16);
   }
   if (FMT <= F_SB6_6)
-    r.b = ld16(a.rec + (size_t)row * nsb * 16 + (g >> 3) * 16);
+    r.b = ld16_w<NT>(a.rec + (size_t)row * nsb * 16 + (g >> 3) * 16);
   if (FMT == F_SB6_5) r.h.x = a.hb[(size_t)row * ng + g];
   if (FMT == F_SB6_6 || FMT == F_SYM6)
     r.h = *reinterpret_cast<const uint2*>(a.hb + (size_t)row * ng * 2 + g * 2);
@@ -76,7 +76,7 @@ struct RawF16 {
 template <int FMT> struct RawOf { using T = Raw; };
 template <> struct RawOf<F_F16> { using T = RawF16; };
 
-template <int FMT, class Args>
+template <int FMT, bool NT = true, class Args>
 __device__ __forceinline__ void load_raw(const Args& a, int row, int ng,
                                          int nsb, int g, RawF16& r) {
   const uint8_t* p = a.q + ((size_t)row * a.in + g * 32) * 2;

@@ -62,6 +62,23 @@ __device__ __forceinline__ uint4 ld16(const void* p) {
   return *reinterpret_cast<const uint4*>(p);
 }
 
+#ifndef RWKVQ_NT_LOADS
+#define RWKVQ_NT_LOADS 1
+#endif
+typedef unsigned int u32x4_nt_t __attribute__((ext_vector_type(4)));
+// 16-byte load of packed weight codes.  NT: a non-temporal (streaming)
+// load (the codes are read once per launch).
+template <bool NT>
+__device__ __forceinline__ uint4 ld16_w(const void* p) {
+  if constexpr (NT && RWKVQ_NT_LOADS) {
+    u32x4_nt_t v =
+        __builtin_nontemporal_load(reinterpret_cast<const u32x4_nt_t*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+  } else {
+    return ld16(p);
+  }
+}
+
 // Nibble byte pair -> two fp16 lanes holding 1024 + code:
 // result low half = 0x6400 | (lo nibble of byte j of w) [| high bits],
 // high half = 0x6400 | (hi nibble of byte j of w).
