@@ -95,11 +95,12 @@ __device__ __forceinline__ void x_group(const float* __restrict__ xp,
 }
 
 // ILV: interleaved row order (the heads); otherwise blocked rows.  The
-// sb6 codes of blocked rows are read with non-temporal loads (1.5B
-// COMPRESSION decode B = 1 1.213 -> 1.169 ms); for the sym / rtn formats,
-// the heads and the batched kernel they were slower (measured).
+// sb6 codes are read with non-temporal loads (1.5B COMPRESSION decode
+// B = 1 1.213 -> 1.169 ms for the blocked rows, the sb6@5 head included
+// 1.118 ms); for the sym / rtn formats (the rtn8 head 28.1 -> 31.6 us) and
+// the batched kernel they were slower (measured).
 template <int FMT, int NN, int RS, bool ILV = false,
-          bool NT = !ILV && FMT <= F_SB6_6>
+          bool NT = FMT <= F_SB6_6>
 __global__ void __launch_bounds__(512)
 gemv_kernel(GemvArgs a) {
   const int lane = threadIdx.x & 63;
