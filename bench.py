@@ -270,7 +270,7 @@ def prefill_bench(model, T, dev, reps=5):
     idx = torch.randint(0, 65536, (1, T), generator=g, device=dev)
     st = model.init_state(1)
     model.forward_stateful(idx, st)              # capture + warm-up
-    gr = model._graphs[(1, T, False, 0)]
+    gr = model._seq_graphs[(1, T, False, 0)]
     _mark()
     torch.cuda.synchronize()
     e0, e1 = (torch.cuda.Event(enable_timing=True) for _ in range(2))

@@ -149,6 +149,18 @@ int rwkvq_x16(const float* x, long x_ld, int cols, int M, int order,
 int rwkvq_gemm_workspace(void* ws, long ws_bytes, int* counters,
                          int n_counters);
 
+/* The launch shape rwkvq_gemm_sb6 / _sym / _rtn8 choose for a GEMM of
+ * these arguments on the current device (with the split-K workspace that
+ * is registered there), without launching anything: plan[0] output rows
+ * per workgroup tile, plan[1] tokens per tile, plan[2] waves along the
+ * rows, plan[3] K groups inside a workgroup (1 or 2), plan[4] workgroups
+ * splitting K per tile, plan[5] workgroups of the launch.  mode as for the
+ * GEMMs (RWKVQ_NO_SPLIT changes the plan).  No counterpart in the
+ * reference (its matmul library picks its own kernel); for tests and
+ * profiles that must know which kernel variant ran. */
+int rwkvq_gemm_plan(int rows, int in, int out_per, int M, int mode,
+                    int* plan);
+
 /* The same GEMM over dense fp16 rows W [rows, in] (in % 128 == 0): the
  * prefill LoRA products.  With epilogue RWKVQ_EPI_PER_SEG each input
  * segment j (rows j*out_per ..) applies the mode in bits 4j..4j+3 of

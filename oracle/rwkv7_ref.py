@@ -12,11 +12,17 @@ shift = 0 on the first call.  Weights are the oracle's exact dequant of the
 checkpoint (codec_ref.dequant_qt), world LoRA transposed after dequant
 (reference: rwkv_quant/formats/codec.py:514-535).
 
-Pinned by tests/test_oracle_forward.py with properties that do not retype
-the formulas: token-by-token == whole-sequence, the w = 1, a = b = 0 case
-equals the closed-form linear-attention sum, the decay identity
-exp(-exp(-softplus(-z) - 0.5)) == exp(-0.606531 sigmoid(z)), and a
-brute-force per-element recurrence on a tiny head.
+Pinned (tests/test_reference_fixtures.py) against the reference's own
+RWKV7Ref forward (fp32, CPU) on a seeded 3-layer model: logits and the
+residual stream after every block within 1e-5 relative, and its
+`perplexity` (calibration/ablation.py:21-69); each of a wrong group-norm
+eps, a bonus without r_k, the output gate's sigmoid after the up product
+and a missing v-residual, planted in a subclass, fails that check.  Also
+pinned by properties (tests/test_oracle_forward.py): token-by-token ==
+whole-sequence, the w = 1, a = b = 0 case equals the closed-form
+linear-attention sum, the decay identity exp(-exp(-softplus(-z) - 0.5)) ==
+exp(-0.606531 sigmoid(z)), and a brute-force per-element recurrence on a
+tiny head.
 """
 import numpy as np
 
@@ -89,6 +95,32 @@ class RWKV7Oracle:
         first = np.zeros((B, 1, C)) if prev is None else prev.reshape(B, 1, C)
         return np.concatenate([first, x[:, :-1]], axis=1), x[:, -1].copy()
 
+    # The time mix is split into the steps below so that a test can plant
+    # a mistake in one of them (a subclass overriding it) and show that
+    # the reference fixture catches it.
+    def _v_residual(self, i, v, v_first, xv):
+        """v + (v_first - v) sigmoid(xv A_v^T B_v^T + v0), layers > 0
+        (reference: rwkv7_ref.py:203-208)."""
+        g = lambda s: self._g(f"blocks.{i}.att.{s}")
+        gate = _sigmoid(xv @ g("v1").T @ g("v2").T + g("v0").reshape(-1))
+        return v + (v_first - v) * gate
+
+    def _gate(self, i, xg):
+        """sigmoid(xg A_g^T) B_g^T (reference: rwkv7_ref.py:212)."""
+        g = lambda s: self._g(f"blocks.{i}.att.{s}")
+        return _sigmoid(xg @ g("g1").T) @ g("g2").T
+
+    def _bonus(self, i, r, k, v):
+        """(sum_n r k r_k) v per head, inputs [B, T, H, N]
+        (reference: rwkv7_ref.py:226-228)."""
+        r_k = self._g(f"blocks.{i}.att.r_k").reshape(self.H, self.N)
+        return (r * k * r_k).sum(-1, keepdims=True) * v
+
+    def _norm_out(self, i, y):
+        """Per-head group norm, eps 64e-5 (reference: rwkv7_ref.py:223-224)."""
+        g = lambda s: self._g(f"blocks.{i}.att.{s}")
+        return group_norm(y, self.H, g("ln_x.weight"), g("ln_x.bias"))
+
     def _tmix(self, i, x, v_first, state):
         g = lambda s: self._g(f"blocks.{i}.att.{s}")
         B, T, C = x.shape
@@ -108,10 +140,9 @@ class RWKV7Oracle:
         if i == 0:
             v_first = v
         else:
-            gate = _sigmoid(xv @ g("v1").T @ g("v2").T + g("v0").reshape(C))
-            v = v + (v_first - v) * gate
+            v = self._v_residual(i, v, v_first, xv)
         a = _sigmoid(xa @ g("a1").T @ g("a2").T + g("a0").reshape(C))
-        gg = _sigmoid(xg @ g("g1").T) @ g("g2").T
+        gg = self._gate(i, xg)
         kk = (k * g("k_k").reshape(C)).reshape(B, T, H, N)
         kk = kk / np.maximum(np.linalg.norm(kk, axis=-1, keepdims=True),
                              1e-12)
@@ -122,10 +153,9 @@ class RWKV7Oracle:
         y, new_state = wkv7(r.reshape(sh), w.reshape(sh), k.reshape(sh),
                             v.reshape(sh), (-kk).reshape(sh),
                             (kk * a).reshape(sh), wkv_state)
-        out = group_norm(y.reshape(B, T, C), H, g("ln_x.weight"),
-                         g("ln_x.bias"))
-        bonus = ((r.reshape(sh) * k.reshape(sh) * g("r_k").reshape(H, N))
-                 .sum(-1, keepdims=True) * v.reshape(sh)).reshape(B, T, C)
+        out = self._norm_out(i, y.reshape(B, T, C))
+        bonus = self._bonus(i, r.reshape(sh), k.reshape(sh),
+                            v.reshape(sh)).reshape(B, T, C)
         out = (out + bonus) * gg
         return out @ g("output.weight").T, v_first, (new_state, new_prev)
 
@@ -136,7 +166,9 @@ class RWKV7Oracle:
         h = np.maximum(xk @ g("key.weight").T, 0.0) ** 2
         return h @ g("value.weight").T, new_prev
 
-    def forward_stateful(self, idx, states, hidden_only=False):
+    def forward_stateful(self, idx, states, hidden_only=False, trace=None):
+        """trace: a list that receives the residual stream after every
+        block, as the reference's `trace` argument (rwkv7_ref.py:261-283)."""
         idx = np.asarray(idx)
         x = self._g("emb.weight")[idx]
         x = layer_norm(x, self._g("blocks.0.ln0.weight"),
@@ -155,7 +187,27 @@ class RWKV7Oracle:
             ff, nc = self._cmix(i, xn2, cshift)
             x = x + ff
             new_states.append((ns, nt, nc))
+            if trace is not None:
+                trace.append(x.copy())
         x = layer_norm(x, self._g("ln_out.weight"), self._g("ln_out.bias"))
         if hidden_only:
             return x, new_states
         return x @ self._g("head.weight").T, new_states
+
+
+def perplexity(orc, data, batch_size=2):
+    """exp(mean NLL) of next-token prediction over rows of `data` [n, L],
+    each row a fresh sequence (reference: calibration/ablation.py:21-69:
+    logits of data[:, :-1], NLL = logsumexp - logit[target])."""
+    data = np.asarray(data)
+    tot, cnt = 0.0, 0
+    for i in range(0, data.shape[0], batch_size):
+        batch = data[i:i + batch_size]
+        lg, _ = orc.forward_stateful(batch[:, :-1],
+                                     orc.init_state(batch.shape[0]))
+        m = lg.max(-1, keepdims=True)
+        lse = (m + np.log(np.exp(lg - m).sum(-1, keepdims=True)))[..., 0]
+        tgt = np.take_along_axis(lg, batch[:, 1:, None], -1)[..., 0]
+        tot += float((lse - tgt).sum())
+        cnt += lse.size
+    return float(np.exp(tot / cnt))

@@ -635,20 +635,35 @@ const SplitWs* current_ws() {
   return g_split_ws[dev].ws ? &g_split_ws[dev] : nullptr;
 }
 
-// Two K groups (8 waves) wherever the tile's registers allow two waves per
-// SIMD (all tiles but 256 x 128) and the step count is even.
+// The launch shape of one GEMM: wave tile 32 * wn rows x 32 * wm tokens,
+// nw waves along N (4, or 8 for the 256 x 128 tile), K split across
+// `split` workgroups per output tile, `one_group` = no second K group
+// inside the workgroup (two independent 4-wave workgroups per CU instead).
+struct GemmPlan {
+  int wn, wm, nw, split;
+  bool one_group;
+};
+
+// K groups inside a workgroup: two (8 waves) wherever the tile's registers
+// allow two waves per SIMD (all tiles but 256 x 128) and the step count of
+// a split run is even.
+int plan_kgroups(const GemmPlan& p, int in) {
+  const bool two = RWKVQ_GEMM_KG == 2 && p.wn * p.wm <= 4 && p.nw == 4;
+  return (two && !p.one_group && (in / kStepK / p.split) % 2 == 0) ? 2 : 1;
+}
+
 template <int FMT, int WN, int WM, int NW = 4>
-int launch_tile(const GemmArgs& a, hipStream_t s, int split = 1,
-                const SplitWs* ws = nullptr, bool one_group = false) {
+int launch_tile(const GemmArgs& a, hipStream_t s, const GemmPlan& p,
+                const SplitWs* ws) {
   GemmArgs b = a;
   b.nt = a.N / (32 * NW * WN);
   b.mt = (a.M + 32 * WM - 1) / (32 * WM);
-  b.split = split;
-  if (split > 1) { b.ws = ws->ws; b.cnt = ws->cnt; }
-  const int grid = b.nt * b.mt * split;
+  b.split = p.split;
+  if (p.split > 1) { b.ws = ws->ws; b.cnt = ws->cnt; }
+  const int grid = b.nt * b.mt * p.split;
   constexpr bool two = RWKVQ_GEMM_KG == 2 && WN * WM <= 4 && NW == 4;
   constexpr int KG2 = two ? 2 : 1;
-  if (two && !one_group && (a.in / kStepK / split) % 2 == 0) {
+  if (two && plan_kgroups(p, a.in) == 2) {
     if (a.xh)
       hipLaunchKernelGGL((gemm_kernel<FMT, WN, WM, KG2, true, NW>),
                          dim3(grid), dim3(64 * NW * KG2), 0, s, b);
@@ -673,17 +688,15 @@ int launch_tile(const GemmArgs& a, hipStream_t s, int split = 1,
 // workgroups.
 // N tiles of 256 rows need out_per % 256 == 0; segment tables take 128-row
 // tiles (their segments are multiples of 128 rows).
-template <int FMT>
-int launch_gemm(const GemmArgs& a, hipStream_t s) {
+GemmPlan plan_gemm(const GemmArgs& a, const SplitWs* ws) {
   auto wgs = [&](int bn, int bm) {
     return (long)(a.N / bn) * ((a.M + bm - 1) / bm);
   };
   const int nsteps = a.in / kStepK;
   const bool wide = a.out_per % 256 == 0 && a.nseg_tab == 0;
-  const SplitWs* ws = a.nosplit ? nullptr : current_ws();
   // 256 x 128 tiles of 8 waves (32 rows x 128 tokens each; x staged once
   // for 256 rows) where they alone give >= 256 workgroups
-  if (wide && wgs(256, 128) >= 256) return launch_tile<FMT, 1, 4, 8>(a, s);
+  if (wide && wgs(256, 128) >= 256) return {1, 4, 8, 1, true};
   if (RWKVQ_GEMM_SPLIT && a.M > 64) {
     // Two 4-wave workgroups per CU (each with its own barrier, so the two
     // waves of a SIMD drift out of phase and overlap decode with MFMA)
@@ -696,9 +709,7 @@ int launch_gemm(const GemmArgs& a, hipStream_t s) {
            nsteps / (2 * split) >= kLongRun && ws && t <= ws->ncnt &&
            t * 2 * split * 128 * 128 * (long)sizeof(float) <= ws->bytes)
       split *= 2;
-    if (t * split >= 512)
-      return launch_tile<FMT, 1, 4>(a, s, split, split > 1 ? ws : nullptr,
-                                    true);
+    if (t * split >= 512) return {1, 4, 4, split, true};
   }
   if (RWKVQ_GEMM_SPLIT && a.M > 64 && nsteps % 2 == 0) {
     const long t = wgs(128, 128);
@@ -707,11 +718,10 @@ int launch_gemm(const GemmArgs& a, hipStream_t s) {
            nsteps % (2 * kMinRun * split) == 0 && ws && t <= ws->ncnt &&
            t * 2 * split * 128 * 128 * (long)sizeof(float) <= ws->bytes)
       split *= 2;
-    if (t * split >= RWKVQ_SPLIT_WGS)
-      return launch_tile<FMT, 1, 4>(a, s, split, ws);
+    if (t * split >= RWKVQ_SPLIT_WGS) return {1, 4, 4, split, false};
   }
-  if (wide && wgs(256, 64) >= 256) return launch_tile<FMT, 2, 2>(a, s);
-  if (wgs(128, 64) >= 256) return launch_tile<FMT, 1, 2>(a, s);
+  if (wide && wgs(256, 64) >= 256) return {2, 2, 4, 1, false};
+  if (wgs(128, 64) >= 256) return {1, 2, 4, 1, false};
   if (RWKVQ_GEMM_SPLIT && wgs(128, 32) < 256 && a.M > 32 && nsteps >= 4 &&
       ws) {
     // few output tiles even at 128 x 32 (e.g. the LoRA down products):
@@ -722,10 +732,24 @@ int launch_gemm(const GemmArgs& a, hipStream_t s) {
            t <= ws->ncnt &&
            t * 2 * split * 128 * 64 * (long)sizeof(float) <= ws->bytes)
       split *= 2;
-    if (split > 1 && t * split >= 192)
-      return launch_tile<FMT, 1, 2>(a, s, split, ws);
+    if (split > 1 && t * split >= 192) return {1, 2, 4, split, false};
   }
-  return launch_tile<FMT, 1, 1>(a, s);
+  return {1, 1, 4, 1, false};
+}
+
+const SplitWs* gemm_ws(const GemmArgs& a) {
+  return a.nosplit ? nullptr : current_ws();
+}
+
+template <int FMT>
+int launch_gemm(const GemmArgs& a, hipStream_t s) {
+  const SplitWs* ws = gemm_ws(a);
+  const GemmPlan p = plan_gemm(a, ws);
+  if (p.nw == 8) return launch_tile<FMT, 1, 4, 8>(a, s, p, ws);
+  if (p.wn == 1 && p.wm == 4) return launch_tile<FMT, 1, 4>(a, s, p, ws);
+  if (p.wn == 2 && p.wm == 2) return launch_tile<FMT, 2, 2>(a, s, p, ws);
+  if (p.wn == 1 && p.wm == 2) return launch_tile<FMT, 1, 2>(a, s, p, ws);
+  return launch_tile<FMT, 1, 1>(a, s, p, ws);
 }
 
 int check_gemm(int rows, int in, int out_per, int M, long x_ld, int mode,
@@ -1078,9 +1102,27 @@ int rwkvq_gemm_f16_grouped(int nseg, const uint16_t* const* w,
   // segments' step counts differ
   auto wgs = [&](int bm) { return (long)(tot / 128) * ((M + bm - 1) / bm); };
   if (wgs(128) >= 256)
-    return launch_tile<F_F16, 1, 4>(a, s, 1, nullptr, true);
-  if (wgs(64) >= 256) return launch_tile<F_F16, 1, 2>(a, s, 1, nullptr, true);
-  return launch_tile<F_F16, 1, 1>(a, s, 1, nullptr, true);
+    return launch_tile<F_F16, 1, 4>(a, s, {1, 4, 4, 1, true}, nullptr);
+  if (wgs(64) >= 256)
+    return launch_tile<F_F16, 1, 2>(a, s, {1, 2, 4, 1, true}, nullptr);
+  return launch_tile<F_F16, 1, 1>(a, s, {1, 1, 4, 1, true}, nullptr);
+}
+
+int rwkvq_gemm_plan(int rows, int in, int out_per, int M, int mode,
+                    int* plan) {
+  if (!plan) return RWKVQ_ERR_ARG;
+  const int st = check_gemm(rows, in, out_per, M, (long)(rows / out_per) * in,
+                            mode, kStepK);
+  if (st) return st;
+  GemmArgs a = make_args(rows, in, out_per, nullptr, 0, nullptr, M, mode);
+  const GemmPlan p = plan_gemm(a, gemm_ws(a));
+  plan[0] = 32 * p.nw * p.wn;
+  plan[1] = 32 * p.wm;
+  plan[2] = p.nw;
+  plan[3] = plan_kgroups(p, in);
+  plan[4] = p.split;
+  plan[5] = (rows / plan[0]) * ((M + plan[1] - 1) / plan[1]) * p.split;
+  return RWKVQ_OK;
 }
 
 }  // extern "C"

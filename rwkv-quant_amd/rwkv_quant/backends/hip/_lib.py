@@ -42,6 +42,7 @@ SIGNATURES = {
     "rwkvq_gemv_f16_seg": [_P, _I, _P, _I, _P, _L, _P, _I, _I, _P],
     "rwkvq_gemm_f16_seg": [_P, _I, _P, _I, _P, _L, _P, _I, _I, _I, _P],
     "rwkvq_gemm_workspace": [_P, _L, _P, _I],
+    "rwkvq_gemm_plan": [_I, _I, _I, _I, _I, _P],
     "rwkvq_gemm_f16_grouped": [_I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P],
     "rwkvq_gemm_dual_f16seg": [_I, _I, _P, _P, _P, _P, _I, _I, _I, _P, _L, _P,
                                _I, _P, _I, _P, _P, _L, _P, _I, _I, _I, _P],
@@ -135,11 +136,20 @@ def call(name, *args):
         raise TypeError(f"{name}: {len(args)} arguments, the C entry point "
                         f"takes {len(SIGNATURES[name])}")
     if name.startswith("rwkvq_gemm_") and name != "rwkvq_gemm_workspace":
+        # (rwkvq_gemm_plan too: the plan depends on the workspace)
         ensure_gemm_workspace()
     st = getattr(load(), name)(*args)
     if st != RWKVQ_OK:
         raise HipKernelError(f"{name}: status {st} "
                              f"({ERRORS.get(st, 'hip error')})")
+
+
+def gemm_plan(rows, in_features, out_per, M, mode=0):
+    """The tile plan of a quantized GEMM (rwkvq_gemm_plan) as a dict."""
+    out = (ctypes.c_int * 6)()
+    call("rwkvq_gemm_plan", rows, in_features, out_per, M, mode, out)
+    return dict(zip(("tile_rows", "tile_tokens", "waves", "kgroups",
+                     "split", "workgroups"), list(out)))
 
 
 def ptr(t):

@@ -33,6 +33,7 @@ Runtime switches (module attributes, as the reference's FUSE flags):
   USE_GRAPH   replay decode steps from a captured HIP graph
 """
 import ctypes
+from collections import OrderedDict
 
 import torch
 
@@ -56,6 +57,8 @@ WKV_PREP_FUSED = True          # chunked prefill: per-channel prep inside the
 X16_PREFILL = True             # prefill GEMM inputs written as fp16 in the
                                # GEMM's pair order by their producers
 LORA_GEMV_ROWS = 32            # decode-batch rows per LoRA-down GEMV launch
+MAX_SEQ_GRAPHS = 8             # captured forward_stateful graphs kept (LRU);
+                               # each owns its logits and two state sets
 
 _LORA = ("w1", "w2", "a1", "a2", "v1", "v2", "g1", "g2")
 
@@ -171,6 +174,34 @@ class _Work:
             self.xk16 = torch.empty(N, C, **h)
             self.hk16 = torch.empty(N, ffn, **h)
             self.h16 = torch.empty(N, rp, **h)
+        self.device = device
+        self.wkv_ops = None
+
+    def wkv_ops_buffer(self, H):
+        """Chunk-operator workspace of the chunked WKV scan, sized once for
+        the largest need of any split N = B * T (T >= WKV_CHUNK_MIN_T), so
+        it is never reallocated: HIP graphs captured for one (B, T) keep
+        pointing at it while other shapes of the same N run (allocated by
+        the warm-up run that precedes any capture)."""
+        if self.wkv_ops is None:
+            self.wkv_ops = torch.empty(wkv_ops_floats(self.N, H),
+                                       dtype=torch.float32,
+                                       device=self.device)
+        return self.wkv_ops
+
+
+def wkv_chunk_slots(B, T):
+    """Chunks per head of the chunked scan: ceil(T / 16) rounded up to a
+    multiple of 3 (the scan applies three chunks per step)."""
+    return B * (-(-(-(-T // 16)) // 3) * 3)
+
+
+def wkv_ops_floats(N, H):
+    """Operator floats of the chunked scan for the worst split of N rows
+    into B sequences of T >= WKV_CHUNK_MIN_T tokens."""
+    slots = max([wkv_chunk_slots(B, N // B) for B in range(1, N + 1)
+                 if N % B == 0 and N // B >= WKV_CHUNK_MIN_T] or [0])
+    return max(1, slots * H * WKV_CHUNK_OPS)
 
 
 class QuantTMix:
@@ -577,7 +608,8 @@ class QuantRWKV7:
         self.ranks = {b: A.shape[0] for b, (A, _) in
                       self.blocks[-1].tmix.lora.items()}
         self._work = {}
-        self._graphs = {}
+        self._graphs = {}              # decode step graphs by batch size
+        self._seq_graphs = OrderedDict()   # forward graphs by shape (LRU)
         torch.cuda.synchronize(dev)
 
     # ------------------------------------------------------------ state
@@ -705,12 +737,7 @@ class QuantRWKV7:
         N, C, H = B * T, self.n_embd, self.n_head
         if T >= WKV_CHUNK_MIN_T and WKV_PREP_FUSED:
             # prep folded into the chunk operators: two launches
-            need = B * H * (-(-(-(-T // 16)) // 3) * 3) * WKV_CHUNK_OPS
-            ops = getattr(wk, "wkv_ops", None)
-            if ops is None or ops.numel() < need:
-                # allocated by the warm-up run that precedes any capture
-                ops = wk.wkv_ops = torch.empty(need, dtype=torch.float32,
-                                               device=self.device)
+            ops = wk.wkv_ops_buffer(H)
             _lib.call("rwkvq_wkv7_prefill_chunked", _lib.ptr(wk.rkv),
                       _lib.ptr(wk.yl["w"]), _lib.ptr(wk.yl["a"]),
                       None if layer0 else _lib.ptr(wk.yl["v"]),
@@ -730,12 +757,7 @@ class QuantRWKV7:
                   _lib.ptr(wk.w), _lib.ptr(wk.kp), _lib.ptr(wk.vp),
                   _lib.ptr(wk.aa), _lib.ptr(wk.bb), N, C, self.head_size, st)
         if T >= WKV_CHUNK_MIN_T:
-            need = B * H * (-(-(-(-T // 16)) // 3) * 3) * WKV_CHUNK_OPS
-            ops = getattr(wk, "wkv_ops", None)
-            if ops is None or ops.numel() < need:
-                # allocated by the warm-up run that precedes any capture
-                ops = wk.wkv_ops = torch.empty(need, dtype=torch.float32,
-                                               device=self.device)
+            ops = wk.wkv_ops_buffer(H)
             _lib.call("rwkvq_wkv7_scan_chunked", _lib.ptr(wk.rkv), 3 * C,
                       _lib.ptr(wk.w), _lib.ptr(wk.kp), _lib.ptr(wk.vp),
                       _lib.ptr(wk.aa), _lib.ptr(wk.bb), C, _lib.ptr(wkv_in),
@@ -814,10 +836,14 @@ class QuantRWKV7:
     def _replay_seq(self, idx, states, last_only, tail_only):
         B, T = idx.shape
         key = (B, T, bool(last_only), int(tail_only))
-        g = self._graphs.get(key)
+        g = self._seq_graphs.get(key)
         if g is None:
             g = self._capture_seq(*key)
-            self._graphs[key] = g
+            self._seq_graphs[key] = g
+            while len(self._seq_graphs) > MAX_SEQ_GRAPHS:
+                self._seq_graphs.popitem(last=False)
+        else:
+            self._seq_graphs.move_to_end(key)
         g["idx"].copy_(idx)
         self._load_states(g["in"], states)
         g["graph"].replay()

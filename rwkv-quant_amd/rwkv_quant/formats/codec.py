@@ -195,3 +195,108 @@ def is_transposed(manifest, key):
     if "transposed" in m:
         return bool(m["transposed"])
     return is_raw_lora_world(key) and manifest.get("naming") == "world"
+
+
+# ------------------------------------------------ relayouts for consumers
+
+def pack_mlx_affine(codes, bits):
+    """Codes [..., 32] (0 .. 2^bits - 1) -> u32 [..., bits]: the 32 codes of
+    a group as one LSB-first bit stream of 32 * bits bits (code p occupies
+    stream bits p*bits .. p*bits + bits - 1, crossing word boundaries), the
+    container of MLX's affine `quantized_matmul` with group size 32
+    (reference: codec.py:313-329)."""
+    codes = np.asarray(codes)
+    if codes.shape[-1] != 32:
+        raise ValueError("MLX affine groups hold 32 codes")
+    lead = codes.shape[:-1]
+    c = codes.astype(np.uint32).reshape(-1, 32, 1)
+    planes = ((c >> np.arange(bits, dtype=np.uint32)) & 1).astype(np.uint8)
+    stream = np.packbits(planes.reshape(-1, 32 * bits), axis=-1,
+                         bitorder="little")            # [G, 4 * bits] bytes
+    words = stream.view("<u4").astype(np.uint32)
+    return words.reshape(lead + (bits,))
+
+
+def unpack_mlx_affine(words, bits, nb):
+    """u32 [..., nb * bits] -> codes [..., nb, 32] (inverse of
+    pack_mlx_affine; reference: codec.py:332-346)."""
+    w = np.ascontiguousarray(np.asarray(words, dtype=np.uint32))
+    lead = w.shape[:-1]
+    stream = w.reshape(-1, bits).astype("<u4").view(np.uint8)
+    planes = np.unpackbits(stream, axis=-1, bitorder="little")
+    planes = planes.reshape(-1, 32, bits).astype(np.uint32)
+    codes = (planes << np.arange(bits, dtype=np.uint32)).sum(-1)
+    return codes.astype(np.uint32).reshape(lead + (nb, 32))
+
+
+def _sb6_codes_scales(codes_packed, qsqm, d, dm, shape, gs, sb, nb, qh, qh2):
+    """Unsigned codes [OUT, IN] and the per-block fp32 scale / min of an
+    sb6 tensor, exactly as the format's dequant forms them:
+    s = max(f32(f16(qs * d)), 1e-8), m = f32(f16(qm * dm))."""
+    OUT, IN = shape
+    NB = IN // gs if nb is None else nb
+    q = unpack_nib_block(codes_packed, gs).astype(np.uint32)
+    if qh is not None:
+        q += unpack_bitplane(qh, IN).astype(np.uint32) << 4
+    if qh2 is not None:
+        q += unpack_bitplane(qh2, IN).astype(np.uint32) << 5
+    qsqm = np.asarray(qsqm)
+    qs = unpack6(qsqm[..., :6], 8).reshape(OUT, NB).astype(np.float32)
+    qm = unpack6(qsqm[..., 6:], 8).reshape(OUT, NB).astype(np.float32) - 31
+    dd = np.repeat(np.asarray(d).astype(np.float32), sb, axis=1)
+    ddm = np.repeat(np.asarray(dm).astype(np.float32), sb, axis=1)
+    s = np.maximum((qs * dd).astype(np.float16).astype(np.float32),
+                   np.float32(1e-8))
+    m = (qm * ddm).astype(np.float16)
+    return q, s, m, NB
+
+
+def sb6_to_mlx_affine(codes_packed, qsqm, d, dm, *, shape, gs, sb, nb=None,
+                      qh=None, qh2=None):
+    """sb6 -> (wq u32 [OUT, NB*bits], scales f16 [OUT, NB], biases f16
+    [OUT, NB], bits) for an affine w = q * scale + bias consumer with
+    group 32.  The codes are moved, not requantized; scale and bias are the
+    format's own per-block values, which are fp16 by construction.  The one
+    difference: a block whose scale is the 1e-8 clamp stores scale 0
+    (1e-8 is below fp16's smallest subnormal), off by at most 63e-8
+    (reference: codec.py:349-387)."""
+    if gs != 32:
+        raise ValueError(f"the affine relayout takes gs 32, not {gs}")
+    OUT, IN = shape
+    bits = 4 + (qh is not None) + (qh2 is not None)
+    q, s, m, NB = _sb6_codes_scales(codes_packed, qsqm, d, dm, shape, gs, sb,
+                                    nb, qh, qh2)
+    wq = pack_mlx_affine(q.reshape(OUT, NB, gs), bits).reshape(OUT, NB * bits)
+    return wq, s.astype(np.float16), m, bits
+
+
+def sb6_to_k3(codes_packed, qsqm, d, dm, *, shape, gs, sb, nb=None, qh=None,
+              qh2=None):
+    """sb6 -> (qblk, qsqm_k3, ddm, xbits), the block-interleaved layout of
+    the reference's Metal loader (reference: codec.py:390-435):
+      qblk[row]    per block: 16 nibble bytes [+ 4 bytes qh] [+ 4 bytes qh2]
+      qsqm_k3[row] per block: qs, qm as int8 (the +31 bias removed)
+      ddm[row]     per superblock: d, dm (fp16)
+    A byte permutation plus the qs/qm widening (2 bytes per block against
+    1.5)."""
+    if gs != 32:
+        raise ValueError(f"the K3 layout takes gs 32, not {gs}")
+    OUT, IN = shape
+    NB = IN // gs if nb is None else nb
+    blocks = [np.asarray(codes_packed).reshape(OUT, NB, 16)]
+    for plane in (qh, qh2):
+        if plane is not None:
+            blocks.append(np.asarray(plane).reshape(OUT, NB, 4))
+    qblk = np.concatenate(blocks, axis=2).reshape(OUT, -1)
+    qsqm = np.asarray(qsqm)
+    qs = unpack6(qsqm[..., :6], 8).reshape(OUT, NB)
+    qm = (unpack6(qsqm[..., 6:], 8).reshape(OUT, NB).astype(np.int8)
+          - np.int8(31))
+    qsqm_k3 = np.empty((OUT, NB, 2), np.uint8)
+    qsqm_k3[..., 0] = qs
+    qsqm_k3[..., 1] = qm.view(np.uint8)
+    ddm = np.empty((OUT, np.asarray(d).shape[1], 2), np.float16)
+    ddm[..., 0] = d
+    ddm[..., 1] = dm
+    return (np.ascontiguousarray(qblk), qsqm_k3.reshape(OUT, -1),
+            ddm.reshape(OUT, -1), len(blocks) - 1)

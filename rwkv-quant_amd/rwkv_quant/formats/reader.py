@@ -37,4 +37,21 @@ def load_raw(path):
         naming=m["naming"], n_layer=m["n_layer"], n_embd=m["n_embd"],
         head_size=m["head_size"], vocab_size=m["vocab_size"],
         tensors=tensors, config_repr=m.get("config_repr", ""),
-        config=None, tokenizer=m.get("tokenizer"))
+        config=config_from_json(m.get("config")),
+        tokenizer=m.get("tokenizer"))
+
+
+def config_from_json(d):
+    """Manifest `config` (writer.config_to_json) -> QuantConfig; None for
+    files that carry none (reference: reader.py:96-111)."""
+    if d is None:
+        return None
+    from ..calibration.group_config import QuantConfig
+    return QuantConfig(
+        clip_percentiles=d.get("clip_percentiles"),
+        outlier_fracs=d.get("outlier_fracs"),
+        bits_overrides=d.get("bits_overrides"),
+        group_scale=d.get("group_scale"),
+        group_scale_mode=d.get("group_scale_mode"),
+        act_stats_path=d.get("act_stats_path"),
+        **d.get("bits", {}))
