@@ -291,6 +291,26 @@ int rwkvq_wkv7_scan_chunked(const float* r, long r_ld, const float* w,
                             int T, int H, int head_size, float* ws,
                             long ws_floats, void* stream);
 
+/* rwkvq_wkv7_scan_chunked without a workspace argument, for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving
+ * loops, harnesses that forbid hipMalloc).  No counterpart in the
+ * reference.  The chunk operators live in a library-owned device array of
+ * 64 MiB per GPU (allocated with the code object, held until the process
+ * ends): B * H * NC * 6400 floats must fit in it (NC = ceil(T / 16)
+ * rounded up to a multiple of 3), i.e. B * H * NC <= 2621 (1.5B: T <= 1296
+ * at B = 1; 2.9B: T <= 1008), else RWKVQ_ERR_SIZE.  Calls on one GPU share
+ * that array: calls that overlap in time (different streams) race; calls
+ * in one stream are ordered.  Nothing in it needs to start at zero (each
+ * call writes every operator it reads).  Same results as
+ * rwkvq_wkv7_scan_chunked, bit for bit. */
+int rwkvq_wkv7_scan_chunked_noalloc(const float* r, long r_ld,
+                                    const float* w, const float* k,
+                                    const float* v, const float* a,
+                                    const float* b, long ld,
+                                    const float* state_in, float* state_out,
+                                    float* y, long y_ld, int B, int T, int H,
+                                    int head_size, void* stream);
+
 /* Prefill time-mix core from the projections: the per-channel inputs of
  * rwkvq_wkv_prep (w, k' -> kp, v' -> vp, a, b; v_first written on layer 0,
  * read otherwise) computed inside the chunk-operator kernel, then the

@@ -17,6 +17,8 @@
 //         (group norm per head, two-pass, eps 64e-5)
 #include "rwkvq_common.h"
 
+#include <mutex>
+
 using namespace rwkvq;
 
 namespace {
@@ -1073,6 +1075,34 @@ void launch_lerp_f16(int order, int rows, hipStream_t s, const float* x,
 
 }  // namespace
 
+// Chunk-operator scratch of rwkvq_wkv7_scan_chunked_noalloc: a module-
+// global device array (one copy per GPU, alive until the process ends), so
+// that entry point allocates nothing.  Host code never passes `scratch`
+// itself to a kernel (on the host it names a stand-in, not a device
+// address): scratch_base() resolves the current device's copy with
+// hipGetSymbolAddress once per device and every launch uses that pointer.
+constexpr long kScratchFloats = 16L << 20;      // 64 MiB
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+namespace {
+float* g_scratch_base[64];
+std::once_flag g_scratch_once[64];
+
+int scratch_base(float** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+    return RWKVQ_ERR_LAUNCH;
+  std::call_once(g_scratch_once[dev], [dev] {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) == hipSuccess)
+      g_scratch_base[dev] = static_cast<float*>(p);
+  });
+  if (!g_scratch_base[dev]) return RWKVQ_ERR_LAUNCH;
+  *out = g_scratch_base[dev];
+  return RWKVQ_OK;
+}
+}  // namespace
+
 extern "C" {
 
 int rwkvq_layer_norm(const float* x, const float* w, const float* b, float* y,
@@ -1171,6 +1201,27 @@ int rwkvq_wkv7_scan_chunked(const float* r, long r_ld, const float* w,
                      state_in ? state_in : state_out, state_out, y, y_ld, T,
                      H, NC);
   return ok_launch();
+}
+
+int rwkvq_wkv7_scan_chunked_noalloc(const float* r, long r_ld,
+                                    const float* w, const float* k,
+                                    const float* v, const float* a,
+                                    const float* b, long ld,
+                                    const float* state_in, float* state_out,
+                                    float* y, long y_ld, int B, int T, int H,
+                                    int head_size, void* stream) {
+  if (B <= 0 || T <= 0 || H <= 0 || head_size != kHead)
+    return RWKVQ_ERR_ARG;
+  const long NC = ((T + kCL - 1) / kCL + 2) / 3 * 3;
+  if ((long)B * H * NC * kOpsFloats > kScratchFloats) return RWKVQ_ERR_SIZE;
+  float* ws = nullptr;
+  const int st = scratch_base(&ws);
+  if (st) return st;
+  // every operator slot the scan reads is written by the operator kernel
+  // of the same call, so nothing in the scratch has to start at zero
+  return rwkvq_wkv7_scan_chunked(r, r_ld, w, k, v, a, b, ld, state_in,
+                                 state_out, y, y_ld, B, T, H, head_size, ws,
+                                 kScratchFloats, stream);
 }
 
 int rwkvq_wkv7_prefill_chunked(const float* rkv, const float* yw,

@@ -65,6 +65,8 @@ SIGNATURES = {
                         _I, _I, _I, _P],
     "rwkvq_wkv7_scan_chunked": [_P, _L, _P, _P, _P, _P, _P, _L, _P, _P, _P,
                                 _L, _I, _I, _I, _I, _P, _L, _P],
+    "rwkvq_wkv7_scan_chunked_noalloc": [_P, _L, _P, _P, _P, _P, _P, _L, _P,
+                                        _P, _P, _L, _I, _I, _I, _I, _P],
     "rwkvq_wkv7_prefill_chunked": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                    _I, _P, _P, _P, _P, _P, _I, _I, _I, _I,
                                    _P, _L, _P],
