@@ -13,9 +13,12 @@
 //
 // Decode: a code byte pair becomes an fp16 pair 1024 + q with v_perm_b32 +
 // v_and_or_b32 (high-bit planes are rotated into bits 4/5 with
-// v_alignbit_b32); v_dot2_f32_f16 multiplies by the fp16 x pair and
-// accumulates in fp32.  The accumulator starts at -1024 * sum(x), so it
-// ends at sum(q * x) exactly up to fp32 rounding.  Block scales follow the
+// v_alignbit_b32), and one packed fp16 subtraction (exact) leaves the
+// signed integer codes.  x is staged per 32-column group as an fp16 hi +
+// lo pair of x * 2^e (a power of two per group, so no fp16 range limit):
+// two v_dot2_f32_f16 per code pair multiply the codes by hi and by lo with
+// exact products and fp32 sums, so the block sums carry x to about 22 bits
+// (fp32 x within the fp32 rounding of the sums).  Block scales follow the
 // format: s = f32(f16(qs * d)) (sb6 also m = f32(f16(qm * dm)), s clamped at
 // 1e-8), identical to the reference arithmetic
 // (reference: rwkv_quant/formats/codec.py:183-257,
@@ -58,9 +61,13 @@ struct GemvArgs {
   float* seg_y[8];
 };
 
-// Convert one lane's 32 x values of group g into the format's 16 fp16
-// pairs and the three block sums (A, B halves in fp16-rounded values, and
-// the fp32 sum used by the sb6 min term).
+// Convert one lane's 32 x values of group g into the format's pair order
+// as an fp16 hi + lo split of x * 2^e: hi = f16(x 2^e), lo = f16(x 2^e - hi),
+// so hi + lo holds x to about 22 bits.  The power of two 2^e (exact) puts
+// the group's largest |x| in [2^14, 2^15): no fp16 overflow whatever the
+// range of x, and lo stays a normal fp16 down to 2^-17 of that maximum.
+// dst: 16 hi pairs, then 16 lo pairs; sums: the fp32 sum of x (the sb6
+// min term) and 2^-e.
 template <int FMT>
 __device__ __forceinline__ void x_group(const float* __restrict__ xp,
                                         uint32_t* __restrict__ dst,
@@ -72,27 +79,38 @@ __device__ __forceinline__ void x_group(const float* __restrict__ xp,
     xv[4 * t] = f.x; xv[4 * t + 1] = f.y; xv[4 * t + 2] = f.z;
     xv[4 * t + 3] = f.w;
   }
-  float sa = 0.f, sb = 0.f, sf = 0.f;
-  uint32_t pk[16];
+  float amax = 0.f, sf = 0.f;
+#pragma unroll
+  for (int c = 0; c < 32; ++c) {
+    amax = fmaxf(amax, fabsf(xv[c]));
+    sf += xv[c];
+  }
+  // inf / nan (amax not finite) keep e = 0 and propagate through the dot
+  int e = 0;
+  if (amax > 0.f && amax <= 3.0e38f) e = min(14 - ilogbf(amax), 100);
+  const float sc = ldexpf(1.f, e);
+  uint32_t hi[16], lo[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     int c0, c1;
     x_cols<FMT>(i, c0, c1);
-    pk[i] = pack_h2(xv[c0], xv[c1]);
-    const float s2 = h2_lo(pk[i]) + h2_hi(pk[i]);
-    if (i < 8) sa += s2; else sb += s2;
+    const float a0 = xv[c0] * sc, a1 = xv[c1] * sc;
+    hi[i] = pack_h2(a0, a1);
+    lo[i] = pack_h2(a0 - h2_lo(hi[i]), a1 - h2_hi(hi[i]));
   }
 #pragma unroll
-  for (int c = 0; c < 32; ++c) sf += xv[c];
-#pragma unroll
-  for (int q = 0; q < 4; ++q)
+  for (int q = 0; q < 4; ++q) {
     reinterpret_cast<uint4*>(dst)[q] =
-        make_uint4(pk[4 * q], pk[4 * q + 1], pk[4 * q + 2], pk[4 * q + 3]);
-  const float mb = magic_bias<FMT>();
-  sums[0] = -mb * sa;
-  sums[1] = -mb * sb;
-  sums[2] = sf;
+        make_uint4(hi[4 * q], hi[4 * q + 1], hi[4 * q + 2], hi[4 * q + 3]);
+    reinterpret_cast<uint4*>(dst)[4 + q] =
+        make_uint4(lo[4 * q], lo[4 * q + 1], lo[4 * q + 2], lo[4 * q + 3]);
+  }
+  sums[0] = sf;
+  sums[1] = ldexpf(1.f, -e);
 }
+
+constexpr int kXWords = 32;   // staged words per (input row, group)
+constexpr int kXSums = 2;     // staged floats per (input row, group)
 
 // ILV: interleaved row order (the heads); otherwise blocked rows.  The
 // sb6 codes are read with non-temporal loads (1.5B COMPRESSION decode
@@ -117,11 +135,11 @@ gemv_kernel(GemvArgs a) {
   const int row_base = wg_row0 + rgi * a.rpw;
   const int nsb = a.in >> 8;
 
-  // x of this workgroup's segment, staged once per workgroup as fp16 pairs
-  // [NN][ng][16] followed by the sums [NN][ng][3] (dynamic LDS)
+  // x of this workgroup's segment, staged once per workgroup as fp16
+  // hi / lo pairs [NN][ng][32] followed by the sums [NN][ng][2] (dynamic LDS)
   extern __shared__ uint32_t smem[];
   uint32_t* s_xh = smem;
-  float* s_xs = reinterpret_cast<float*>(smem + NN * ng * 16);
+  float* s_xs = reinterpret_cast<float*>(smem + NN * ng * kXWords);
   __shared__ float red[8 * RS * NN];
 
   // first weight batch in flight before x is fetched: the two memory round
@@ -155,29 +173,38 @@ gemv_kernel(GemvArgs a) {
     if (n < a.n) {
       x_group<FMT>(a.x + (size_t)n * a.x_ld + (size_t)seg * a.in +
                        (size_t)gg * 32,
-                   s_xh + (size_t)item * 16, s_xs + (size_t)item * 3);
+                   s_xh + (size_t)item * kXWords,
+                   s_xs + (size_t)item * kXSums);
     } else {
 #pragma unroll
-      for (int q = 0; q < 16; ++q) s_xh[(size_t)item * 16 + q] = 0u;
-      s_xs[item * 3] = s_xs[item * 3 + 1] = s_xs[item * 3 + 2] = 0.f;
+      for (int q = 0; q < kXWords; ++q) s_xh[(size_t)item * kXWords + q] = 0u;
+      s_xs[item * kXSums] = 0.f;
+      s_xs[item * kXSums + 1] = 1.f;
     }
   }
   __syncthreads();
-  uint32_t xh[NN][16];
-  float xsa[NN], xsb[NN], xsf[NN];
+  uint32_t xh[NN][16], xl[NN][16];
+  float xsf[NN], xsc[NN];
 #pragma unroll
   for (int n = 0; n < NN; ++n) {
-    const uint4* src = reinterpret_cast<const uint4*>(s_xh + (n * ng + gl) * 16);
+    const uint4* src =
+        reinterpret_cast<const uint4*>(s_xh + (n * ng + gl) * kXWords);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       uint4 v = src[q];
       xh[n][4 * q] = v.x; xh[n][4 * q + 1] = v.y;
       xh[n][4 * q + 2] = v.z; xh[n][4 * q + 3] = v.w;
+      v = src[4 + q];
+      xl[n][4 * q] = v.x; xl[n][4 * q + 1] = v.y;
+      xl[n][4 * q + 2] = v.z; xl[n][4 * q + 3] = v.w;
     }
-    xsa[n] = s_xs[(n * ng + gl) * 3];
-    xsb[n] = s_xs[(n * ng + gl) * 3 + 1];
-    xsf[n] = s_xs[(n * ng + gl) * 3 + 2];
+    xsf[n] = s_xs[(n * ng + gl) * kXSums];
+    xsc[n] = s_xs[(n * ng + gl) * kXSums + 1];
   }
+  // the decoder's fp16 pairs hold 1024 + code (+ the storage bias):
+  // subtracting it in fp16 is exact and leaves the signed integer codes
+  const _Float16 mbh = (_Float16)magic_bias<FMT>();
+  const h2_t bias2 = {mbh, mbh};
 
   // per-lane constants for sb6 scale extraction (block k of its superblock)
   const int kb = g & 7;
@@ -199,15 +226,26 @@ gemv_kernel(GemvArgs a) {
     for (int j = 0; j < RS; ++j) {
       uint32_t h[16];
       decode_raw<FMT>(cur[j], h);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) h[i] = h2_bits(as_h2(h[i]) - bias2);
+      // block sums of code * x (scaled by 2^e): the products are exact in
+      // fp32, four independent chains
       float dA[NN], dB[NN];
 #pragma unroll
       for (int n = 0; n < NN; ++n) {
-        float ca = xsa[n], cb = xsb[n];
+        float ah = 0.f, al = 0.f, bh = 0.f, bl = 0.f;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) ca = dot2(h[i], xh[n][i], ca);
+        for (int i = 0; i < 8; ++i) {
+          ah = dot2(h[i], xh[n][i], ah);
+          al = dot2(h[i], xl[n][i], al);
+        }
 #pragma unroll
-        for (int i = 8; i < 16; ++i) cb = dot2(h[i], xh[n][i], cb);
-        dA[n] = ca; dB[n] = cb;
+        for (int i = 8; i < 16; ++i) {
+          bh = dot2(h[i], xh[n][i], bh);
+          bl = dot2(h[i], xl[n][i], bl);
+        }
+        dA[n] = (ah + al) * xsc[n];
+        dB[n] = (bh + bl) * xsc[n];
       }
       if (FMT <= F_SB6_6) {
         const uint32_t rr[4] = {cur[j].b.x, cur[j].b.y, cur[j].b.z,
@@ -373,33 +411,81 @@ bgemv_kernel(GemvArgs a) {
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) acc[b][rt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
+  // One 128-column step: x of the step (per input row, scaled by a power of
+  // two that puts its largest |x| in [2^14, 2^15), so fp16 cannot
+  // overflow) and the weights, each as fp16 hi + lo; per sub-step the
+  // products hi.hi + hi.lo + lo.hi go through the matrix core (lo.lo,
+  // below 2^-22 of the product, is dropped), the step's sum is unscaled
+  // and added to the fp32 accumulator.
+  constexpr bool kWLo = FMT != F_RTN8 && FMT != F_F16;
   auto mma_step = [&](int st, RawT (&w_raw)[RT], float4 (&xv)[NB][8]) {
-    half8_t bx[NB][4];
+    half8_t bh[NB][4], bl[NB][4];
+    float isc[NB];
 #pragma unroll
-    for (int b = 0; b < NB; ++b)
+    for (int b = 0; b < NB; ++b) {
+      float amax = 0.f;
+#pragma unroll
+      for (int t = 0; t < 8; ++t)
+        amax = fmaxf(fmaxf(fmaxf(amax, fabsf(xv[b][t].x)), fabsf(xv[b][t].y)),
+                     fmaxf(fabsf(xv[b][t].z), fabsf(xv[b][t].w)));
+      // the step's four groups of input row i sit in lanes i + 16 q
+      amax = fmaxf(amax, __shfl_xor(amax, 16));
+      amax = fmaxf(amax, __shfl_xor(amax, 32));
+      int e = 0;
+      if (amax > 0.f && amax <= 3.0e38f) e = min(14 - ilogbf(amax), 100);
+      const float sc = ldexpf(1.f, e);
+      isc[b] = ldexpf(1.f, -e);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         int ca, cb;
         step_cols<FMT>(j, ca, cb);
-        uint4 xp = x_pairs<FMT>(xv[b][ca >> 2], xv[b][cb >> 2]);
-        if (!xon[b]) xp = make_uint4(0u, 0u, 0u, 0u);
-        bx[b][j] = __builtin_bit_cast(half8_t, xp);
+        float4 A = xv[b][ca >> 2], B = xv[b][cb >> 2];
+        A.x *= sc; A.y *= sc; A.z *= sc; A.w *= sc;
+        B.x *= sc; B.y *= sc; B.z *= sc; B.w *= sc;
+        const float4 Ah = make_float4(f16_round(A.x), f16_round(A.y),
+                                      f16_round(A.z), f16_round(A.w));
+        const float4 Bh = make_float4(f16_round(B.x), f16_round(B.y),
+                                      f16_round(B.z), f16_round(B.w));
+        uint4 xh = x_pairs<FMT>(Ah, Bh);
+        uint4 xl = x_pairs<FMT>(
+            make_float4(A.x - Ah.x, A.y - Ah.y, A.z - Ah.z, A.w - Ah.w),
+            make_float4(B.x - Bh.x, B.y - Bh.y, B.z - Bh.z, B.w - Bh.w));
+        if (!xon[b]) xh = xl = make_uint4(0u, 0u, 0u, 0u);
+        bh[b][j] = __builtin_bit_cast(half8_t, xh);
+        bl[b][j] = __builtin_bit_cast(half8_t, xl);
       }
+    }
     const int kb = (gw + 4 * st + q) & 7;   // group within its superblock
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-      uint32_t w[16];
-      dequant_group<FMT>(w_raw[rt], kb, w);
+      uint32_t wh[16], wl[16];
+      dequant_group_hilo<FMT>(w_raw[rt], kb, wh, wl);
+      f32x4_t d[NB];
+#pragma unroll
+      for (int b = 0; b < NB; ++b) d[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const half8_t av = __builtin_bit_cast(
-            half8_t,
-            make_uint4(w[4 * j], w[4 * j + 1], w[4 * j + 2], w[4 * j + 3]));
+        const half8_t ah = __builtin_bit_cast(
+            half8_t, make_uint4(wh[4 * j], wh[4 * j + 1], wh[4 * j + 2],
+                                wh[4 * j + 3]));
+        const half8_t al = __builtin_bit_cast(
+            half8_t, make_uint4(wl[4 * j], wl[4 * j + 1], wl[4 * j + 2],
+                                wl[4 * j + 3]));
 #pragma unroll
-        for (int b = 0; b < NB; ++b)
-          acc[b][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-              av, bx[b][j], acc[b][rt], 0, 0, 0);
+        for (int b = 0; b < NB; ++b) {
+          d[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh[b][j], d[b],
+                                                        0, 0, 0);
+          d[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl[b][j], d[b],
+                                                        0, 0, 0);
+          if (kWLo)
+            d[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh[b][j], d[b],
+                                                          0, 0, 0);
+        }
       }
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[b][rt][v] += d[b][v] * isc[b];
     }
   };
 
@@ -517,19 +603,17 @@ int launch_bg_rt(GemvArgs a, hipStream_t s) {
   return hipGetLastError() == hipSuccess ? RWKVQ_OK : RWKVQ_ERR_LAUNCH;
 }
 
-// K slices: two 128-column steps per wave where up to 16 waves cover K,
-// else 16 slices (K a multiple of 2048), else the largest divisor <= 8 of
-// the step count.  More than 8 slices take 1024-thread workgroups of
-// 16-row tiles (128 VGPRs a lane).  Otherwise row tiles are the widest
-// that keep >= 256 workgroups and divide a segment.
+// K slices: two 128-column steps per wave where up to 8 waves cover K,
+// else the largest divisor <= 8 of the step count.  Row tiles are the
+// widest that keep >= 256 workgroups and divide a segment.
 template <int FMT>
 int launch_bg(GemvArgs a, hipStream_t s) {
   const int steps = a.in / 128;
+  // at most 8 K slices: the hi / lo operands need more than the 128 VGPRs
+  // a lane of a 16-wave workgroup has
   int ks;
-  if (steps % 2 == 0 && steps / 2 <= 16) {
+  if (steps % 2 == 0 && steps / 2 <= 8) {
     ks = steps / 2;
-  } else if (steps % 16 == 0) {
-    ks = 16;
   } else {
     ks = 8;
     while (steps % ks) --ks;
@@ -547,7 +631,6 @@ int launch_bg(GemvArgs a, hipStream_t s) {
   }
   a.ks = ks;
   a.rpw = steps / ks;
-  if (ks > 8) return launch_bg_rt<FMT, 1, 16>(a, s);
   // 64-row tiles only pay for the int8 formats (measured: sb6 heads are
   // faster with 32-row tiles, int8 heads with 64)
   constexpr bool kWide = FMT == F_SYM8 || FMT == F_RTN8;
@@ -594,17 +677,20 @@ int launch_rs(GemvArgs a, hipStream_t s) {
                    rows_waves > 16384 &&
                    (long)grid.x * rows_per_wg == (long)a.rows;
   const int ng = a.in / 32;
-  // up to 8 input rows per launch (each weight read once per chunk); the
-  // staged x must fit the LDS budget of 96 KiB per workgroup
-  int chunk = 8;
-  while (chunk > 1 && (size_t)chunk * ng * (16 + 3) * 4 > 96 * 1024) chunk >>= 1;
+  // up to 4 input rows per launch (each weight read once per chunk; the
+  // hi / lo x of 8 rows would not fit the VGPRs); the staged x must fit
+  // the LDS budget of 96 KiB per workgroup
+  int chunk = 4;
+  while (chunk > 1 &&
+         (size_t)chunk * ng * (kXWords + kXSums) * 4 > 96 * 1024)
+    chunk >>= 1;
   for (int n0 = 0; n0 < a.n; n0 += chunk) {
     GemvArgs b = a;
     b.x = a.x + (size_t)n0 * a.x_ld;
     b.y = a.y + (size_t)n0 * a.rows;
     b.n = a.n - n0 < chunk ? a.n - n0 : chunk;
     const int nn = b.n <= 1 ? 1 : b.n <= 2 ? 2 : b.n <= 4 ? 4 : 8;
-    const size_t lds = (size_t)nn * ng * (16 + 3) * 4;
+    const size_t lds = (size_t)nn * ng * (kXWords + kXSums) * 4;
     switch (nn) {
       case 1:
         if (ilv)
@@ -618,13 +704,7 @@ int launch_rs(GemvArgs a, hipStream_t s) {
         else
           hipLaunchKernelGGL((gemv_kernel<FMT, 2, RS>), grid, block, lds, s, b);
         break;
-      case 4: hipLaunchKernelGGL((gemv_kernel<FMT, 4, RS>), grid, block, lds, s, b); break;
-      default:
-        if constexpr (RS == 2)   // 8 columns x 4 rows would spill VGPRs
-          hipLaunchKernelGGL((gemv_kernel<FMT, 8, RS>), grid, block, lds, s, b);
-        else
-          return RWKVQ_ERR_ARG;
-        break;
+      default: hipLaunchKernelGGL((gemv_kernel<FMT, 4, RS>), grid, block, lds, s, b); break;
     }
   }
   return hipGetLastError() == hipSuccess ? RWKVQ_OK : RWKVQ_ERR_LAUNCH;
@@ -642,7 +722,7 @@ int launch_fmt(GemvArgs a, hipStream_t s) {
   a.rg = a.ks >= 8 ? 1 : 8 / a.ks;  // <= 8 waves per workgroup share x
   // small matrices: 2-row batches keep more waves in flight; large ones
   // amortise the lane-resident x over 4-row batches
-  if ((long)a.rows * a.ks <= 8192 || a.out_per % 4 || a.n > 4)
+  if ((long)a.rows * a.ks <= 8192 || a.out_per % 4 || a.n > 2)
     return launch_rs<FMT, 2>(a, s);
   return launch_rs<FMT, 4>(a, s);
 }

@@ -184,6 +184,70 @@ __device__ __forceinline__ void dequant_group(const Raw& r, int kb,
   }
 }
 
+// The format's fp32 weights of one (row, group) split into fp16 hi + lo
+// pairs (hi = f16(w), lo = f16(w - hi): w to about 22 bits), in the
+// decoder's pair order.  sb6 w = q s + m, sym w = q s (s, m the fp32
+// values of the format's fp16 block scales); rtn8 and dense fp16 weights
+// are fp16 already (lo = 0).  Returns false where lo is identically 0.
+template <int FMT>
+__device__ __forceinline__ bool dequant_group_hilo(const Raw& r, int kb,
+                                                   uint32_t whi[16],
+                                                   uint32_t wlo[16]) {
+  decode_raw<FMT>(r, whi);
+  const _Float16 mbh = (_Float16)magic_bias<FMT>();
+  const h2_t bias = {mbh, mbh};
+#pragma unroll
+  for (int i = 0; i < 16; ++i) whi[i] = h2_bits(as_h2(whi[i]) - bias);
+  if (FMT == F_RTN8) {                 // the int8 codes; row scale later
+#pragma unroll
+    for (int i = 0; i < 16; ++i) wlo[i] = 0u;
+    return false;
+  }
+  float s0, s1, m = 0.f;
+  if (FMT <= F_SB6_6) {
+    const uint32_t rr[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
+    const int qs_word = (6 * kb) >> 5, qs_sh = (6 * kb) & 31;
+    const int qm_word = (48 + 6 * kb) >> 5, qm_sh = (48 + 6 * kb) & 31;
+    uint32_t lo = qs_word == 0 ? rr[0] : rr[1];
+    uint32_t hi = qs_word == 0 ? rr[1] : rr[2];
+    const uint32_t qsv = __builtin_amdgcn_alignbit(hi, lo, (uint32_t)qs_sh) & 63u;
+    lo = qm_word == 1 ? rr[1] : rr[2];
+    hi = qm_word == 1 ? rr[2] : rr[3];
+    const uint32_t qmv = __builtin_amdgcn_alignbit(hi, lo, (uint32_t)qm_sh) & 63u;
+    const float d = f16_bits_to_f32(rr[3] & 0xFFFFu);
+    const float dm = f16_bits_to_f32(rr[3] >> 16);
+    s0 = s1 = fmaxf(f16_round((float)qsv * d), 1e-8f);
+    m = f16_round((float)((int)qmv - 31) * dm);
+  } else {                             // sym6 / sym8: two 16-column blocks
+    const float d = f16_bits_to_f32(r.dd);
+    s0 = f16_round((float)(int8_t)(r.s & 0xFFu) * d);
+    s1 = f16_round((float)(int8_t)((r.s >> 8) & 0xFFu) * d);
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const float s = i < 8 ? s0 : s1;
+    const float wa = fmaf(h2_lo(whi[i]), s, m);
+    const float wb = fmaf(h2_hi(whi[i]), s, m);
+    whi[i] = pack_h2(wa, wb);
+    wlo[i] = pack_h2(wa - h2_lo(whi[i]), wb - h2_hi(whi[i]));
+  }
+  return true;
+}
+
+template <int FMT>
+__device__ __forceinline__ bool dequant_group_hilo(const RawF16& r, int,
+                                                   uint32_t whi[16],
+                                                   uint32_t wlo[16]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    whi[4 * i] = r.q[i].x; whi[4 * i + 1] = r.q[i].y;
+    whi[4 * i + 2] = r.q[i].z; whi[4 * i + 3] = r.q[i].w;
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) wlo[i] = 0u;
+  return false;
+}
+
 // Dense fp16 rows: the stored values are the weights.
 template <int FMT>
 __device__ __forceinline__ void dequant_group(const RawF16& r, int,

@@ -14,12 +14,13 @@ Same contract as the reference Metal classes
   Fused(lins)(xstack [K, IN])  -> [K, out_per]: the K row-concatenated
                                matrices in one launch
 
-Batches of up to GEMM_MIN_BATCH_NB - 1 rows take the GEMV kernel (which
-reads each weight once per 16 or 32 rows), except from GEMM_MID_BATCH rows
-on (and from GEMM_WIDE_BATCH rows for outputs of GEMM_WIDE_ROWS rows or
-more) where the MFMA GEMM is the faster one; larger batches (prefill) take
-the MFMA GEMM with the dequantization fused into its operand load.  Every path runs a HIP kernel of librwkvq_hip; nothing here computes
-on the CPU.
+Batches of up to GEMM_MIN_BATCH_NB - 1 rows take the GEMV kernels (fp32
+x and exact weights to about 22 bits, like the reference's k3 / k3nb
+kernels; the batched one reads each weight once per 16 or 32 rows);
+larger batches (prefill) take the MFMA GEMM with the dequantization fused
+into its operand load and fp16 operands, as the reference's prefill
+matmul.  Every path runs a HIP kernel of librwkvq_hip; nothing here
+computes on the CPU.
 """
 import numpy as np
 import torch
@@ -29,12 +30,15 @@ from .repack import rtn8_device, sb6_device, sym_device
 
 GEMM_MIN_BATCH_NB = 128          # reference: quant_linear_gw.py:153
 GEMM_ROW_TILE = 128              # output rows per MFMA GEMM tile
-# Below GEMM_MIN_BATCH_NB the batched GEMV re-reads x once per 16..32 output
-# rows; measured on MI355X (2.9B shapes), the MFMA GEMM (x staged once per
-# 128 rows) is faster from 33 rows on every shape, and from 17 rows where
-# the output has at least GEMM_WIDE_ROWS rows (enough 128-row tiles).
-GEMM_MID_BATCH = 33
-GEMM_WIDE_BATCH = 17
+# Below GEMM_MIN_BATCH_NB rows the fp16-operand MFMA GEMM is faster than
+# the batched GEMV from 33 rows on every 2.9B shape, and from 17 rows where
+# the output has at least GEMM_WIDE_ROWS rows (measured on MI355X), but it
+# rounds x and W to fp16 (the reference keeps fp32 x below 128 rows).
+# GEMM_MID_BATCH / GEMM_WIDE_BATCH = GEMM_MIN_BATCH_NB keep the precise
+# GEMV for every decode batch; lowering them trades that precision for
+# speed (33 / 17 were the measured cross-over points).
+GEMM_MID_BATCH = GEMM_MIN_BATCH_NB
+GEMM_WIDE_BATCH = GEMM_MIN_BATCH_NB
 GEMM_WIDE_ROWS = 4096
 
 

@@ -168,7 +168,8 @@ def test_gemm_f16_per_segment_epilogue():
 def test_gemv_f16_segments(n, ranks):
     """The decode LoRA down products in one launch: segment j of the
     stacked fp16 factors reads input slot j and writes its own output with
-    its own epilogue; against the float64 product of the fp16 operands."""
+    its own epilogue; against the float64 product of the fp16 factors and
+    the fp32 x (x is carried as an fp16 hi + lo split)."""
     g = torch.Generator().manual_seed(n + len(ranks))
     K = 2048
     A = [(torch.randn(r, K, generator=g) * 0.05).half() for r in ranks]
@@ -188,9 +189,9 @@ def test_gemv_f16_segments(n, ranks):
     _lib.call("rwkvq_gemv_f16_seg", _lib.ptr(Ad), len(ranks), rows, K,
               _lib.ptr(xd[:, s0]), 6 * K, yp, n, sm, _lib.stream_handle())
     for j, (Aj, m) in enumerate(zip(A, modes)):
-        ref = fns[m](xs[:, s0 + j].half().double().numpy()
+        ref = fns[m](xs[:, s0 + j].double().numpy()
                      @ Aj.double().numpy().T)
-        assert relmax(ys[j].cpu().numpy(), ref) < 2e-5, j
+        assert relmax(ys[j].cpu().numpy(), ref) < 1e-5, j
 
 
 def test_gemv_f16_segments_errors():
