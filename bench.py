@@ -15,8 +15,13 @@ metric: algorithmic bytes of the set (canonical .rwkvq buffers + x + y) per
 second of step time, in GB/s.  roofline: the dominant kernel (the int8
 head GEMV) -- algorithmic bytes per launch over its mean launch time,
 measured with HIP events on the launch stream, against the 8 TB/s HBM
-peak.  cpu_baseline: the CPU oracle (numpy dequant + fp32 GEMV) on a
-bounded sample of the same set, timed on this host.
+peak and against the stream-read ceiling measured in the same run
+(stream_ceiling).  Decode lines carry their HBM roofline (algorithmic bytes
+per step / step time), prefill lines the GEMM kernels' FLOP rate against
+the MFMA peak.  cpu_baseline: the CPU oracle (numpy dequant + fp32 GEMV)
+on a bounded sample of the same set at the host's thread share and at one
+thread, a torch-CPU GEMV on pre-dequantized weights, and the oracle's
+decode / prefill of the 1.5B model, timed on this host.
 """
 import argparse
 import json
@@ -72,7 +77,12 @@ def algorithmic_bytes(qts):
     return per
 
 
-def cpu_baseline(qts, budget_s=15.0):
+# The GPU box gives one GPU a share of 16 host threads, whatever the
+# visible core count; the n-thread CPU runs use min(affinity, 16).
+CPU_SHARE = 16
+
+
+def cpu_baseline(qts, budget_s=15.0, cores=None):
     """Reference-faithful CPU path: oracle dequant to fp32 + fp32 GEMV."""
     import numpy as np
     from oracle import codec_ref as cr
@@ -80,8 +90,8 @@ def cpu_baseline(qts, budget_s=15.0):
         from threadpoolctl import threadpool_limits
     except ImportError:                                  # pragma: no cover
         threadpool_limits = None
-    cores = len(os.sched_getaffinity(0))
-    cores = min(cores, 16)
+    if cores is None:
+        cores = min(len(os.sched_getaffinity(0)), CPU_SHARE)
     per = algorithmic_bytes(qts)
     rng = np.random.default_rng(1)
     xs = {n: rng.standard_normal((1, qt.shape[1])).astype(np.float32)
@@ -227,10 +237,11 @@ def trace_summary(path, top=40):
               f"{mn / 1e3:8.2f} {mx / 1e3:8.2f} {100 * tot / total:5.1f}%")
 
 
-def decode_bench(preset, batches, n_tok, dev, shape="1.5b"):
+def decode_bench(preset, batches, n_tok, dev, shape="1.5b", ceiling=None):
     """ms per decode step of the 1.5B- (or 2.9B-) shaped model (graph
     replay, state carried between steps, fresh uniform-random token ids
-    each step)."""
+    each step), with the HBM roofline of each batch (algorithmic bytes per
+    step from the checkpoint's stored tensors, decode_step_bytes)."""
     import torch
     from rwkv_quant.backends.hip.quant_model import QuantRWKV7
     from rwkv_quant.models.synthetic import SHAPES as MS, quantized_model
@@ -239,6 +250,7 @@ def decode_bench(preset, batches, n_tok, dev, shape="1.5b"):
         k: v for k, v in MS[shape].items() if k != "vocab"},
         vocab=MS[shape]["vocab"])
     model = QuantRWKV7(ck, device=dev)
+    step_bytes = {B: decode_step_bytes(ck, B) for B in batches}
     del ck
     build_s = time.time() - t0
     out = {"build_s": round(build_s, 1)}
@@ -259,6 +271,7 @@ def decode_bench(preset, batches, n_tok, dev, shape="1.5b"):
         ms = e0.elapsed_time(e1) / n_tok
         out[f"b{B}_ms_per_step"] = round(ms, 4)
         out[f"b{B}_tok_s"] = round(B * 1e3 / ms, 1)
+    add_decode_roofline(out, step_bytes, ceiling)
     return model, out
 
 
@@ -346,13 +359,223 @@ def weight_elems(shape):
     return L * per - 2 * D * rk["v"] + sh["vocab"] * D
 
 
+MFMA_PEAK_TFLOPS = 2500.0        # dense fp16 / bf16, MI355X datasheet
+
+
 def pp512(model, dev, T=512, shape="1.5b"):
     """Prefill of T tokens with the projection FLOP rate
-    (2 * weight_elems(shape) per token)."""
+    (2 * weight_elems(shape) per token): end to end, and over the GEMM
+    kernels alone (gemm_only_ms) against the dense fp16 MFMA peak."""
     pf = prefill_bench(model, T, dev)
     flop = 2 * weight_elems(shape) * T
+    pf["flop"] = flop
     pf["tflop_s"] = round(flop / (pf["ms"] * 1e-3) / 1e12, 2)
+    gm = gemm_only_ms(model, T, dev)
+    pf["gemm_ms"] = round(gm, 3)
+    pf["gemm_tflop_s"] = round(flop / (gm * 1e-3) / 1e12, 1)
+    pf["gemm_frac_mfma_peak"] = round(pf["gemm_tflop_s"] / MFMA_PEAK_TFLOPS,
+                                      4)
     return pf
+
+
+def stream_ceiling(dev, gib=2, blocks=(512, 1024, 2048, 4096, 8192),
+                   reps=10):
+    """Measured HBM read ceiling: rwkvq_probe_stream_read (16-byte loads,
+    the GEMVs' access pattern) over a 2 GiB buffer, the best rate over a
+    sweep of workgroup counts, HIP events on the launch stream."""
+    import torch
+    from rwkv_quant.backends.hip import _lib
+    nbytes = gib << 30
+    buf = torch.ones(nbytes, dtype=torch.uint8, device=dev)
+    out = torch.empty(max(blocks), dtype=torch.int32, device=dev)
+    st = torch.cuda.current_stream()
+    rates = {}
+    for nb in blocks:
+        for _ in range(2):
+            _lib.call("rwkvq_probe_stream_read", _lib.ptr(buf), nbytes,
+                      _lib.ptr(out), nb, _lib.stream_handle(st))
+        e0, e1 = (torch.cuda.Event(enable_timing=True) for _ in range(2))
+        e0.record(st)
+        for _ in range(reps):
+            _lib.call("rwkvq_probe_stream_read", _lib.ptr(buf), nbytes,
+                      _lib.ptr(out), nb, _lib.stream_handle(st))
+        e1.record(st)
+        torch.cuda.synchronize()
+        rates[nb] = nbytes * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9
+    del buf
+    torch.cuda.empty_cache()
+    best = max(rates, key=rates.get)
+    return {"gbs": round(rates[best], 1), "workgroups": best,
+            "bytes": nbytes,
+            "sweep_gbs": {str(k): round(v, 1) for k, v in rates.items()},
+            "kernel": "rwkvq_probe_stream_read (16-byte loads, 256 threads "
+                      "per workgroup)"}
+
+
+def qt_bytes(qt):
+    """Canonical `.rwkvq` bytes of one stored tensor (every field)."""
+    import torch
+    b = 0
+    for v in vars(qt).values():
+        if torch.is_tensor(v):
+            b += v.numel() * v.element_size()
+    return b
+
+
+def decode_step_bytes(ck, B):
+    """Algorithmic HBM bytes of one decode step of B sequences: every
+    stored tensor once (canonical file bytes; the embedding table only for
+    the B rows gathered), the fp32 WKV state read and written, the two
+    token-shift rows read and written per layer, the fp32 logits out."""
+    H, N = ck.n_embd // ck.head_size, ck.head_size
+    w = 0
+    for key, qt in ck.tensors.items():
+        if key == "emb.weight":
+            w += B * qt_bytes(qt) // qt.shape[0]
+        else:
+            w += qt_bytes(qt)
+    state = ck.n_layer * B * (H * N * N * 4 * 2 + 2 * ck.n_embd * 4 * 2)
+    return w + state + B * ck.vocab_size * 4
+
+
+def add_decode_roofline(out, step_bytes, ceiling):
+    """Per batch: achieved GB/s = algorithmic bytes per step / step time,
+    against the 8 TB/s datasheet peak and the measured stream ceiling."""
+    for key in list(out):
+        if key.endswith("_ms_per_step"):
+            b = key[:-len("_ms_per_step")]
+            byt = step_bytes[int(b[1:])]
+            gbs = byt / (out[key] * 1e-3) / 1e9
+            out[f"{b}_bytes_per_step"] = byt
+            out[f"{b}_gbs"] = round(gbs, 1)
+            out[f"{b}_frac_hbm_peak"] = round(gbs / HBM_PEAK_GBS, 4)
+            if ceiling:
+                out[f"{b}_frac_stream_ceiling"] = round(gbs / ceiling, 4)
+
+
+def gemm_only_ms(model, T, dev, reps=5):
+    """Time of the prefill's GEMM kernels alone (every projection GEMM of
+    every layer, the LoRA GEMMs and the head, on fp16 inputs of the right
+    shapes), replayed from a HIP graph: the denominator of the prefill
+    MFMA roofline."""
+    import torch
+    from rwkv_quant.backends.hip import _lib, quant_model as qm
+    N = T
+    wk = model._work_for(N)
+    for t in (wk.xs16, wk.o16, wk.xk16, wk.hk16, wk.h16):
+        t.zero_()
+    wk.x.zero_()
+    wk.xo.zero_()
+    logits = torch.empty(N, model.vocab_size, device=dev)
+
+    def run():
+        for blk in model.blocks:
+            orders = qm._x16_orders(blk)
+            if orders is None:
+                raise RuntimeError("layer without the fp16 GEMM path")
+            tm, cm = blk.tmix, blk.cmix
+            o_r, o_o, o_k, o_v = orders
+            tm.run_rkv_lora_x16(wk, o_r)
+            tm.o_proj.apply_into(wk.o16, wk.x, mode=_lib.EPI_ADD | _lib.X_F16,
+                                 n=N)
+            cm.key.apply_into(wk.xk16, wk.hk16, n=N,
+                              mode=(_lib.EPI_RELU2 | _lib.X_F16 | _lib.Y_F16
+                                    | (o_v << _lib.Y_ORDER_SHIFT)))
+            cm.value.apply_into(wk.hk16, wk.x, mode=_lib.EPI_ADD | _lib.X_F16,
+                                n=N)
+        model.head.apply_into(wk.xo, logits, n=N)
+
+    run()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        run()
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = (torch.cuda.Event(enable_timing=True) for _ in range(2))
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def cpu_info():
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "cpus_visible": os.cpu_count(),
+            "cpus_affinity": len(os.sched_getaffinity(0))}
+
+
+def cpu_model_baseline(dev, budget_s=20.0):
+    """The CPU oracle (numpy float64 restatement of the forward) on the
+    1.5B compression model: ms per decode token at batch 1 and prefill
+    tok/s on a 16-token prompt, on the host's cores."""
+    import numpy as np
+    from oracle.rwkv7_ref import RWKV7Oracle
+    from rwkv_quant.models.synthetic import (SHAPES as MS, checkpoint_to,
+                                             quantized_model)
+    ck = quantized_model("compression", seed=0, device=dev, **{
+        k: v for k, v in MS["1.5b"].items() if k != "vocab"},
+        vocab=MS["1.5b"]["vocab"])
+    ck = checkpoint_to(ck, "cpu")
+    t0 = time.perf_counter()
+    orc = RWKV7Oracle(ck)
+    build = time.perf_counter() - t0
+    del ck
+    ids = np.random.default_rng(5).integers(0, 65536, size=(1, 18))
+    st = orc.init_state(1)
+    t0 = time.perf_counter()
+    _, st = orc.forward_stateful(ids[:, :16], st)
+    pf = time.perf_counter() - t0
+    dec, n = 0.0, 0
+    for t in range(16, 18):
+        t0 = time.perf_counter()
+        _, st = orc.forward_stateful(ids[:, t:t + 1], st)
+        dec += time.perf_counter() - t0
+        n += 1
+        if dec > budget_s:
+            break
+    return {"decode_ms_per_token_b1": round(1e3 * dec / n, 1),
+            "prefill_tok_s_t16": round(16 / pf, 2),
+            "sample": f"oracle (numpy float64) forward of the 1.5B "
+                      f"compression model: a 16-token prompt then {n} "
+                      f"decode token(s); weights dequantized once "
+                      f"({build:.0f} s, untimed)"}
+
+
+def torch_cpu_ceiling(qts, cores, reps=3):
+    """fp32 GEMV on weights dequantized once (untimed), torch CPU: what a
+    CPU reaches when it does not dequantize per call."""
+    import torch
+    from oracle import codec_ref as cr
+    per = algorithmic_bytes(qts)
+    old = torch.get_num_threads()
+    torch.set_num_threads(cores)
+    try:
+        Ws = {n: torch.from_numpy(cr.dequant_qt(qt)) for n, qt in qts.items()}
+        xs = {n: torch.randn(1, qt.shape[1]) for n, qt in qts.items()}
+        for n in Ws:
+            xs[n] @ Ws[n].T
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            for n in Ws:
+                xs[n] @ Ws[n].T
+        t = (time.perf_counter() - t0) / reps
+    finally:
+        torch.set_num_threads(old)
+    f32 = sum(w.numel() * 4 for w in Ws.values())
+    return {"ms_per_set": round(t * 1e3, 2),
+            "set_gbs_algorithmic": round(sum(per.values()) / t / 1e9, 2),
+            "fp32_weight_gbs": round(f32 / t / 1e9, 2), "threads": cores}
 
 
 def main():
@@ -402,7 +625,8 @@ def main():
         bs = tuple(int(b) for b in (args.decode_batches or (
             "1,32" if big else "1,8")).split(","))
         _, dec = decode_bench("compression", bs, args.decode_tokens, dev,
-                              "2.9b" if big else "1.5b")
+                              "2.9b" if big else "1.5b",
+                              stream_ceiling(dev)["gbs"])
         key = "decode_2p9b_compression" if big else "decode_1p5b_compression"
         print(json.dumps({key: dec}), flush=True)
         return
@@ -416,6 +640,7 @@ def main():
         print(json.dumps({"pp2048_2p9b_reduction":
                           pp512(model, dev, 2048, "2.9b")}), flush=True)
         return
+    ceiling = stream_ceiling(dev)
     qts = build_set()
     per = algorithmic_bytes(qts)
     set_bytes = sum(per.values())
@@ -432,7 +657,7 @@ def main():
         "ms_per_step": round(ms_per_step, 5),
         "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "i8/u8 codes, fp16 x pairs, fp32 accumulate",
+        "dtype": "i8/u8 codes, x as fp16 hi+lo (about 22 bits), fp32 accumulate",
         "data": "synthetic (seeded N(0,0.02) weights, 0.1% x20 outlier "
                 "columns, bf16 N(0,1) x)",
         "config": {"workload": "configs[1]: sym@6 cmix key 2048->8192 + "
@@ -448,33 +673,51 @@ def main():
                      "traffic": traffic,
                      "traffic_source": traffic_src,
                      "launch_us": round(kern["head"] * 1e3, 3),
-                     "bytes_per_launch": per["head"]},
+                     "bytes_per_launch": per["head"],
+                     "frac_stream_ceiling": round(achieved / ceiling["gbs"],
+                                                  4)},
+        "stream_ceiling": ceiling,
         "cpu_baseline": None,
     }
     if not args.no_model:
         model, dec = decode_bench("compression", (1, 8), args.decode_tokens,
-                                  dev)
+                                  dev, ceiling=ceiling["gbs"])
         out["decode_1p5b_compression"] = dec
         del model
         torch.cuda.empty_cache()
-        model, dec_r = decode_bench("reduction", (1,), 32, dev)
+        model, dec_r = decode_bench("reduction", (1,), 32, dev,
+                                    ceiling=ceiling["gbs"])
         out["decode_1p5b_reduction"] = dec_r
         out["pp512_1p5b_reduction"] = pp512(model, dev)
         del model
         torch.cuda.empty_cache()
     if not args.no_model and not args.no_2p9b:
         # 2.9B shape, decode at batch 1 and 32, prefill T=2048
-        model, dec = decode_bench("compression", (1, 32), 64, dev, "2.9b")
+        model, dec = decode_bench("compression", (1, 32), 64, dev, "2.9b",
+                                  ceiling["gbs"])
         out["decode_2p9b_compression"] = dec
         del model
         torch.cuda.empty_cache()
-        model, dec_r = decode_bench("reduction", (1,), 32, dev, "2.9b")
+        model, dec_r = decode_bench("reduction", (1,), 32, dev, "2.9b",
+                                    ceiling["gbs"])
         out["decode_2p9b_reduction"] = dec_r
         out["pp2048_2p9b_reduction"] = pp512(model, dev, 2048, "2.9b")
         del model
         torch.cuda.empty_cache()
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(qts)
+        info = cpu_info()
+        cores = min(info["cpus_affinity"], CPU_SHARE)
+        cb = cpu_baseline(qts, cores=cores)
+        one = cpu_baseline(qts, budget_s=6.0, cores=1)
+        cb.update(info)
+        cb["cores_note"] = (f"{cores} threads: the GPU box's host share for "
+                            f"one GPU ({info['cpus_affinity']} visible in "
+                            f"the affinity mask)")
+        cb["one_thread"] = {"value": one["value"], "sample": one["sample"]}
+        cb["torch_f32_predequantized"] = torch_cpu_ceiling(qts, cores)
+        if not args.no_model:
+            cb["model_1p5b_compression"] = cpu_model_baseline(dev)
+        out["cpu_baseline"] = cb
     print(json.dumps(out), flush=True)
 
 

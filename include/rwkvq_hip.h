@@ -442,6 +442,15 @@ int rwkvq_lora_gemv(int n_jobs, const void* const* W, const float* const* x,
                     void* stream);
 
 
+/* ------------------------------------------------------ perplexity
+ * nll[r] = logsumexp(logits[r, :V]) - logits[r, target[r]] for r < rows
+ * (one pass over each row, fixed reduction order); a target outside
+ * [0, V) or a NaN logit gives NaN.  logits 16-byte aligned, ld % 4 == 0.
+ * Replaces: the per-batch NLL of calibration.ablation.perplexity
+ *   (reference: rwkv_quant/calibration/ablation.py:21-69). */
+int rwkvq_nll_rows(const float* logits, long ld, const int64_t* target,
+                   int rows, int V, float* nll, void* stream);
+
 /* ------------------------------------------------------------- probes
  * HBM read ceiling: stream `bytes` (multiple of 16) with 16-byte loads
  * from n_blocks workgroups of 256 threads; out[n_blocks] receives a

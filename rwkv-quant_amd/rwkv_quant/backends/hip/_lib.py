@@ -52,6 +52,7 @@ SIGNATURES = {
     "rwkvq_dequant_rtn8_f32": [_P, _P, _I, _I, _P, _I, _P],
     "rwkvq_dequant_asym_f32": [_P, _P, _P, _I, _I, _I, _P, _I, _P],
     "rwkvq_probe_stream_read": [_P, ctypes.c_long, _P, _I, _P],
+    "rwkvq_nll_rows": [_P, _L, _P, _I, _I, _P, _P],
     "rwkvq_dequant_f16": [_I, _P, _P, _P, _P, _P, _I, _I, _P, _I, _P],
     "rwkvq_gather_rows_f32": [_I, _I, _P, _P, _P, _P, _I, _I, _P, _I, _P,
                               _P],
