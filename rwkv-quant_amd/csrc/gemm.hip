@@ -814,6 +814,18 @@ x16_kernel(const float* __restrict__ x, long x_ld, uint16_t* __restrict__ out,
 
 }  // namespace
 
+namespace rwkvq {
+bool split_workspace(float** ws, long* bytes, int** cnt, int* ncnt) {
+  const SplitWs* w = current_ws();
+  if (!w) return false;
+  *ws = w->ws;
+  *bytes = w->bytes;
+  *cnt = w->cnt;
+  *ncnt = w->ncnt;
+  return true;
+}
+}  // namespace rwkvq
+
 extern "C" {
 
 int rwkvq_x16(const float* x, long x_ld, int cols, int M, int order,

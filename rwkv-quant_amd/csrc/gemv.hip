@@ -59,6 +59,12 @@ struct GemvArgs {
   int nseg_tab, seg_modes;
   int seg_end[8];
   float* seg_y[8];
+  // matrix-core kernel, split-K across workgroups: `split` workgroups
+  // share a row tile, each over its own K slices; partials go to ws,
+  // cnt[tile] counts arrivals (the GEMMs' registered workspace)
+  int split;
+  float* ws;
+  int* cnt;
 };
 
 // Convert one lane's 32 x values of group g into the format's pair order
@@ -69,9 +75,9 @@ struct GemvArgs {
 // dst: 16 hi pairs, then 16 lo pairs; sums: the fp32 sum of x (the sb6
 // min term) and 2^-e.
 template <int FMT>
-__device__ __forceinline__ void x_group(const float* __restrict__ xp,
-                                        uint32_t* __restrict__ dst,
-                                        float* __restrict__ sums) {
+__device__ __forceinline__ void x_group_regs(const float* __restrict__ xp,
+                                             uint32_t hi[16], uint32_t lo[16],
+                                             float& sum, float& isc) {
   float xv[32];
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
@@ -89,7 +95,6 @@ __device__ __forceinline__ void x_group(const float* __restrict__ xp,
   int e = 0;
   if (amax > 0.f && amax <= 3.0e38f) e = min(14 - ilogbf(amax), 100);
   const float sc = ldexpf(1.f, e);
-  uint32_t hi[16], lo[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     int c0, c1;
@@ -98,6 +103,16 @@ __device__ __forceinline__ void x_group(const float* __restrict__ xp,
     hi[i] = pack_h2(a0, a1);
     lo[i] = pack_h2(a0 - h2_lo(hi[i]), a1 - h2_hi(hi[i]));
   }
+  sum = sf;
+  isc = ldexpf(1.f, -e);
+}
+
+template <int FMT>
+__device__ __forceinline__ void x_group(const float* __restrict__ xp,
+                                        uint32_t* __restrict__ dst,
+                                        float* __restrict__ sums) {
+  uint32_t hi[16], lo[16];
+  x_group_regs<FMT>(xp, hi, lo, sums[0], sums[1]);
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     reinterpret_cast<uint4*>(dst)[q] =
@@ -105,8 +120,6 @@ __device__ __forceinline__ void x_group(const float* __restrict__ xp,
     reinterpret_cast<uint4*>(dst)[4 + q] =
         make_uint4(lo[4 * q], lo[4 * q + 1], lo[4 * q + 2], lo[4 * q + 3]);
   }
-  sums[0] = sf;
-  sums[1] = ldexpf(1.f, -e);
 }
 
 constexpr int kXWords = 32;   // staged words per (input row, group)
@@ -117,8 +130,12 @@ constexpr int kXSums = 2;     // staged floats per (input row, group)
 // B = 1 1.213 -> 1.169 ms for the blocked rows, the sb6@5 head included
 // 1.118 ms); for the sym / rtn formats (the rtn8 head 28.1 -> 31.6 us) and
 // the batched kernel they were slower (measured).
+// XD: x loaded and converted per lane (no LDS staging, no barrier) --
+// faster for rows wider than a wave's 2048-column slice, where every
+// workgroup would otherwise stage the whole row (measured: 8192-wide sym6
+// 9.8 -> 9.4 us; slower for 2048-wide rows and the heads).
 template <int FMT, int NN, int RS, bool ILV = false,
-          bool NT = FMT <= F_SB6_6>
+          bool NT = FMT <= F_SB6_6, bool XD = false>
 __global__ void __launch_bounds__(512)
 gemv_kernel(GemvArgs a) {
   const int lane = threadIdx.x & 63;
@@ -168,6 +185,26 @@ gemv_kernel(GemvArgs a) {
                         nsb, gl, cur[j]);
 
   const int seg = !ILV && wg_row0 < a.rows ? wg_row0 / a.out_per : 0;
+  uint32_t xh[NN][16], xl[NN][16];
+  float xsf[NN], xsc[NN];
+  if constexpr (XD) {
+  // each lane converts its own group of x straight from global memory
+  // (L2 after the first wave): no LDS round trip, no barrier before the
+  // first row
+#pragma unroll
+  for (int n = 0; n < NN; ++n) {
+    if (n < a.n) {
+      x_group_regs<FMT>(a.x + (size_t)n * a.x_ld + (size_t)seg * a.in +
+                            (size_t)gl * 32,
+                        xh[n], xl[n], xsf[n], xsc[n]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) xh[n][i] = xl[n][i] = 0u;
+      xsf[n] = 0.f;
+      xsc[n] = 1.f;
+    }
+  }
+  } else {
   for (int item = threadIdx.x; item < NN * ng; item += blockDim.x) {
     const int n = item / ng, gg = item % ng;
     if (n < a.n) {
@@ -183,8 +220,6 @@ gemv_kernel(GemvArgs a) {
     }
   }
   __syncthreads();
-  uint32_t xh[NN][16], xl[NN][16];
-  float xsf[NN], xsc[NN];
 #pragma unroll
   for (int n = 0; n < NN; ++n) {
     const uint4* src =
@@ -200,6 +235,7 @@ gemv_kernel(GemvArgs a) {
     }
     xsf[n] = s_xs[(n * ng + gl) * kXSums];
     xsc[n] = s_xs[(n * ng + gl) * kXSums + 1];
+  }
   }
   // the decoder's fp16 pairs hold 1024 + code (+ the storage bias):
   // subtracting it in fp16 is exact and leaves the signed integer codes
@@ -361,7 +397,8 @@ bgemv_kernel(GemvArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int i = lane & 15, q = lane >> 4;
   const int ng = a.in >> 5, nsb = a.in >> 8;
-  const int row0 = blockIdx.x * 16 * RT;
+  const int tile = blockIdx.x / a.split, sp = blockIdx.x % a.split;
+  const int row0 = tile * 16 * RT;
   // segment of this tile: uniform out_per, or the table (constant-index
   // reads and value selects only)
   int seg = row0 / a.out_per, s_lo = 0;
@@ -377,7 +414,9 @@ bgemv_kernel(GemvArgs a) {
       s_y = past ? a.seg_y[j] : s_y;
     }
   }
-  const int gw = wave * a.rpw * 4;         // first group of the wave's slice
+  // first group of the wave's K slice (slices of all split workgroups of
+  // the tile in order)
+  const int gw = (sp * a.ks + wave) * a.rpw * 4;
   bool xon[NB];
   const float* xr[NB];
 #pragma unroll
@@ -417,7 +456,10 @@ bgemv_kernel(GemvArgs a) {
   // products hi.hi + hi.lo + lo.hi go through the matrix core (lo.lo,
   // below 2^-22 of the product, is dropped), the step's sum is unscaled
   // and added to the fp32 accumulator.
-  constexpr bool kWLo = FMT != F_RTN8 && FMT != F_F16;
+#ifndef RWKVQ_BG_WLO
+#define RWKVQ_BG_WLO 1
+#endif
+  constexpr bool kWLo = RWKVQ_BG_WLO && FMT != F_RTN8 && FMT != F_F16;
   auto mma_step = [&](int st, RawT (&w_raw)[RT], float4 (&xv)[NB][8]) {
     half8_t bh[NB][4], bl[NB][4];
     float isc[NB];
@@ -459,7 +501,13 @@ bgemv_kernel(GemvArgs a) {
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
       uint32_t wh[16], wl[16];
-      dequant_group_hilo<FMT>(w_raw[rt], kb, wh, wl);
+      if (kWLo || FMT == F_RTN8 || FMT == F_F16) {
+        dequant_group_hilo<FMT>(w_raw[rt], kb, wh, wl);
+      } else {                 // fp16 weights (the format's one rounding)
+        dequant_group<FMT>(w_raw[rt], kb, wh);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) wl[i] = 0u;
+      }
       f32x4_t d[NB];
 #pragma unroll
       for (int b = 0; b < NB; ++b) d[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -562,13 +610,55 @@ bgemv_kernel(GemvArgs a) {
     for (int j = 0; j < 8; ++j)
       seg_hi = j == seg ? a.seg_end[j] : seg_hi;
   }
-  for (int idx = threadIdx.x; idx < kRows * 16 * NB; idx += a.ks * 64) {
-    const int n = idx / kRows, r = idx % kRows;   // rows fastest: coalesced
-    if (n >= a.n) break;
+  auto slice_sum = [&](int idx) {
+    const int n = idx / kRows, r = idx % kRows;
     const int e = ((n >> 4) * RT + (r >> 4)) * 256 + (r & 3) * 64 + (n & 15) +
                   16 * ((r & 15) >> 2);
     float v = 0.f;
     for (int k = 0; k < a.ks; ++k) v += red[k * NB * RT * 256 + e];
+    return v;
+  };
+  constexpr int TE = kRows * 16 * NB;        // outputs of a row tile
+  if (a.split > 1) {
+    // Every workgroup stores its partial sums and counts itself in; the
+    // last to arrive adds the partials in split order 0, 1, ... (the same
+    // sum whichever finishes last), applies the epilogue and re-arms the
+    // counter.  Agent-scope relaxed atomics are coherent across the XCDs'
+    // L2s without a cache flush.
+    float* part = a.ws + (size_t)tile * a.split * TE;
+    for (int idx = threadIdx.x; idx < TE; idx += a.ks * 64) {
+      if (idx / kRows >= a.n) break;
+      __hip_atomic_store(part + (size_t)sp * TE + idx, slice_sum(idx),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __shared__ int s_last;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0)
+      s_last = __hip_atomic_fetch_add(a.cnt + tile, 1, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT) ==
+               a.split - 1;
+    __syncthreads();
+    if (!s_last) return;
+    if (threadIdx.x == 0)
+      __hip_atomic_store(a.cnt + tile, 0, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+  }
+  for (int idx = threadIdx.x; idx < kRows * 16 * NB; idx += a.ks * 64) {
+    const int n = idx / kRows, r = idx % kRows;   // rows fastest: coalesced
+    if (n >= a.n) break;
+    float v;
+    if (a.split > 1) {
+      const float* part = a.ws + (size_t)tile * a.split * TE + idx;
+      v = 0.f;
+      for (int q = 0; q < a.split; ++q)
+        v += q == sp ? slice_sum(idx)
+                     : __hip_atomic_load(part + (size_t)q * TE,
+                                         __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      v = slice_sum(idx);
+    }
     const int row = row0 + r;
     if (FMT == F_RTN8) v *= f16_bits_to_f32(a.d[row]);
     float* yp = a.nseg_tab > 0
@@ -585,9 +675,34 @@ bgemv_kernel(GemvArgs a) {
   }
 }
 
+// Split K across workgroups (halving each wave's steps) until the launch
+// has >= RWKVQ_BG_SPLIT_WGS workgroups, where the workspace allows; one
+// 16-row block only (measured: 1.5B decode B = 8 2.15 -> 2.04 ms per step;
+// with two blocks, 2.9B B = 32, 7.47 -> 7.78 ms, so not there).
+#ifndef RWKVQ_BG_SPLIT_WGS
+#define RWKVQ_BG_SPLIT_WGS 256
+#endif
+
 template <int FMT, int RT, int KSMAX, int NB = 1>
 int launch_bg_rt(GemvArgs a, hipStream_t s) {
-  dim3 grid(a.rows / (16 * RT)), block(64 * a.ks);
+  const long tiles = a.rows / (16 * RT);
+  a.split = 1;
+  float* ws;
+  long ws_bytes;
+  int* cnt;
+  int ncnt;
+  if (NB == 1 && split_workspace(&ws, &ws_bytes, &cnt, &ncnt) &&
+      tiles <= ncnt) {
+    const long te = 16L * RT * 16 * NB;
+    while (tiles * a.split < RWKVQ_BG_SPLIT_WGS && a.rpw % 2 == 0 &&
+           tiles * 2 * a.split * te * (long)sizeof(float) <= ws_bytes) {
+      a.split *= 2;
+      a.rpw /= 2;
+    }
+    a.ws = ws;
+    a.cnt = cnt;
+  }
+  dim3 grid(tiles * a.split), block(64 * a.ks);
   for (int n0 = 0; n0 < a.n; n0 += 16 * NB) {
     GemvArgs b = a;
     b.x = a.x + (size_t)n0 * a.x_ld;
@@ -690,17 +805,24 @@ int launch_rs(GemvArgs a, hipStream_t s) {
     b.y = a.y + (size_t)n0 * a.rows;
     b.n = a.n - n0 < chunk ? a.n - n0 : chunk;
     const int nn = b.n <= 1 ? 1 : b.n <= 2 ? 2 : b.n <= 4 ? 4 : 8;
-    const size_t lds = (size_t)nn * ng * (kXWords + kXSums) * 4;
+    // (the interleaved-row kernels always stage x in LDS)
+    const bool xd = a.ks > 1 && !ilv;
+    const size_t lds = xd ? 0 : (size_t)nn * ng * (kXWords + kXSums) * 4;
+    constexpr bool NT = FMT <= F_SB6_6;
     switch (nn) {
       case 1:
         if (ilv)
           hipLaunchKernelGGL((gemv_kernel<FMT, 1, RS, RS == 4>), grid, block, lds, s, b);
+        else if (xd)
+          hipLaunchKernelGGL((gemv_kernel<FMT, 1, RS, false, NT, true>), grid, block, lds, s, b);
         else
           hipLaunchKernelGGL((gemv_kernel<FMT, 1, RS>), grid, block, lds, s, b);
         break;
       case 2:
         if (ilv)
           hipLaunchKernelGGL((gemv_kernel<FMT, 2, RS, RS == 4>), grid, block, lds, s, b);
+        else if (xd)
+          hipLaunchKernelGGL((gemv_kernel<FMT, 2, RS, false, NT, true>), grid, block, lds, s, b);
         else
           hipLaunchKernelGGL((gemv_kernel<FMT, 2, RS>), grid, block, lds, s, b);
         break;

@@ -12,6 +12,11 @@ typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 
 namespace rwkvq {
 
+// The split-K workspace registered on the current device with
+// rwkvq_gemm_workspace (partial tiles + arrival counters), shared by the
+// GEMMs and the batched GEMV; false when none is registered.  Host side.
+bool split_workspace(float** ws, long* bytes, int** cnt, int* ncnt);
+
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t bits16) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
 }

@@ -138,8 +138,10 @@ def call(name, *args):
         # ctypes would pass extra arguments on (as to a varargs function)
         raise TypeError(f"{name}: {len(args)} arguments, the C entry point "
                         f"takes {len(SIGNATURES[name])}")
-    if name.startswith("rwkvq_gemm_") and name != "rwkvq_gemm_workspace":
-        # (rwkvq_gemm_plan too: the plan depends on the workspace)
+    if name.startswith(("rwkvq_gemm_", "rwkvq_gemv_")) and \
+            name != "rwkvq_gemm_workspace":
+        # the GEMMs and the batched GEMV split K through the workspace
+        # (rwkvq_gemm_plan too: the plan depends on it)
         ensure_gemm_workspace()
     st = getattr(load(), name)(*args)
     if st != RWKVQ_OK:
