@@ -101,6 +101,34 @@ int rwkvq_gemv_rtn8(const int8_t* codes, const uint16_t* scale, int rows,
                     int in, int out_per, const float* x, long x_ld, float* y,
                     int n_cols, int epilogue, void* stream);
 
+/* SpQR outliers of the per-row int8 format as CSR per output row:
+ * row_ptr [rows + 1], cols [nnz] (int32), vals [nnz] (bf16 bits, the
+ * stored outlier values; the codes are 0 there).
+ *
+ * rwkvq_gemv_rtn8_spqr: y = epi(x . W^T) with W = codes * scale + the
+ * outliers (out_per = rows).  One or two input rows sum the row's
+ * outliers inside the GEMV (after the row scale, x in fp32); three or
+ * more run the matrix-core GEMV, then rwkvq_spqr_apply.
+ * Replaces: QuantLinearV2.__call__ with outliers and its kernel's CSR loop
+ *   (reference: quant_linear_v2.py:35-84, 322-351).
+ * rwkvq_spqr_apply: y[t, r] = epi(y[t, r] + sum_k vals[k] x[t, cols[k]]),
+ * k over row r's outliers (the tail after a GEMM / GEMV that stored or
+ * accumulated the int8 part); mode RWKVQ_EPI_STORE (plain add), RELU2,
+ * TANH or SIGMOID.
+ * rwkvq_spqr_scatter: w[r, cols[k]] = vals[k] (the dense dequant's
+ * outlier overwrite, codec.py:279-292). */
+int rwkvq_gemv_rtn8_spqr(const int8_t* codes, const uint16_t* scale,
+                         const int* row_ptr, const int* cols,
+                         const uint16_t* vals, int rows, int in,
+                         const float* x, long x_ld, float* y, int n,
+                         int mode, void* stream);
+int rwkvq_spqr_apply(const float* x, long x_ld, const int* row_ptr,
+                     const int* cols, const uint16_t* vals, int rows, int n,
+                     float* y, int mode, void* stream);
+int rwkvq_spqr_scatter(const int* row_ptr, const int* cols,
+                       const uint16_t* vals, int rows, float* w, long ld,
+                       void* stream);
+
 /* ------------------------------------------------------ prefill GEMM
  * y[t, :] = epilogue(x[t] @ W^T) for t < M tokens, on the matrix cores
  * (v_mfma_f32_32x32x16_f16), W decoded from the same device layouts as the

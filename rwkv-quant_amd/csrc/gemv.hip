@@ -65,6 +65,11 @@ struct GemvArgs {
   int split;
   float* ws;
   int* cnt;
+  // lane-dot kernel, rtn8 with SpQR outliers: CSR per output row (row
+  // pointers into columns / bf16 values); null without outliers
+  const int* sp_ptr;
+  const int* sp_col;
+  const uint16_t* sp_val;
 };
 
 // Convert one lane's 32 x values of group g into the format's pair order
@@ -316,6 +321,34 @@ gemv_kernel(GemvArgs a) {
     for (int n = 0; n < NN; ++n)
 #pragma unroll
       for (int j = 0; j < RS; ++j) acc[n][j] = wave_sum_dpp(acc[n][j]);
+    // SpQR tail of the int8 rows (after the row scale): the row's outliers
+    // strided over the lanes of K-slice 0, x read in fp32
+    float osum[NN][RS];
+#pragma unroll
+    for (int n = 0; n < NN; ++n)
+#pragma unroll
+      for (int j = 0; j < RS; ++j) osum[n][j] = 0.f;
+    if (FMT == F_RTN8 && a.sp_ptr && kslice == 0) {
+#pragma unroll
+      for (int j = 0; j < RS; ++j) {
+        const int row = row_of(r0 + j);
+        const bool live = r0 + j < nrows;
+        const int k0 = live ? a.sp_ptr[row] : 0;
+        const int k1 = live ? a.sp_ptr[row + 1] : 0;
+        for (int k = k0 + lane; k < k1; k += 64) {
+          const int c = a.sp_col[k];
+          const float val = __builtin_bit_cast(
+              float, (uint32_t)a.sp_val[k] << 16);
+#pragma unroll
+          for (int n = 0; n < NN; ++n)
+            if (n < a.n)
+              osum[n][j] += val * a.x[(size_t)n * a.x_ld +
+                                      (size_t)seg * a.in + c];
+        }
+#pragma unroll
+        for (int n = 0; n < NN; ++n) osum[n][j] = wave_sum_dpp(osum[n][j]);
+      }
+    }
     if (a.ks > 1) {
       if (lane == 0) {
 #pragma unroll
@@ -346,7 +379,7 @@ gemv_kernel(GemvArgs a) {
           const int row = row_of(r0 + j);
           if (lane != n * RS + j || n >= a.n || r0 + j >= nrows) continue;
           float v = acc[n][j];
-          if (FMT == F_RTN8) v *= f16_bits_to_f32(a.d[row]);
+          if (FMT == F_RTN8) v = v * f16_bits_to_f32(a.d[row]) + osum[n][j];
           float* yp = a.y + (size_t)n * a.rows + row;
           switch (a.mode) {
             case RWKVQ_EPI_ADD: v += *yp; break;
@@ -908,6 +941,38 @@ int rwkvq_gemv_rtn8(const int8_t* codes, const uint16_t* scale, int rows,
   a.x_ld = x_ld > 0 ? x_ld : (long)a.n_seg * in;
   if (a.x_ld < (long)a.n_seg * in) return RWKVQ_ERR_ARG;
   return launch_fmt<F_RTN8>(a, (hipStream_t)stream);
+}
+
+int rwkvq_gemv_rtn8_spqr(const int8_t* codes, const uint16_t* scale,
+                         const int* row_ptr, const int* cols,
+                         const uint16_t* vals, int rows, int in,
+                         const float* x, long x_ld, float* y, int n,
+                         int mode, void* stream) {
+  int st = check_common(rows, in, rows, n, mode);
+  if (st) return st;
+  if (!codes || !scale || !row_ptr || !cols || !vals || !x || !y)
+    return RWKVQ_ERR_ARG;
+  if (x_ld <= 0) x_ld = in;
+  if (x_ld < in) return RWKVQ_ERR_ARG;
+  hipStream_t s = (hipStream_t)stream;
+  if (n > 2) {
+    // the matrix-core rows: GEMV (store / accumulate), then the outlier
+    // tail and the epilogue in rwkvq_spqr_apply
+    st = rwkvq_gemv_rtn8(codes, scale, rows, in, rows, x, x_ld, y, n,
+                         mode == RWKVQ_EPI_ADD ? RWKVQ_EPI_ADD
+                                               : RWKVQ_EPI_STORE,
+                         stream);
+    if (st) return st;
+    return rwkvq_spqr_apply(x, x_ld, row_ptr, cols, vals, rows, n, y,
+                            mode == RWKVQ_EPI_ADD ? RWKVQ_EPI_STORE : mode,
+                            stream);
+  }
+  GemvArgs a{};
+  a.q = reinterpret_cast<const uint8_t*>(codes); a.d = scale; a.x = x; a.y = y;
+  a.rows = rows; a.in = in; a.out_per = rows; a.n_seg = 1;
+  a.mode = mode; a.n = n; a.x_ld = x_ld;
+  a.sp_ptr = row_ptr; a.sp_col = cols; a.sp_val = vals;
+  return launch_fmt<F_RTN8>(a, s);
 }
 
 int rwkvq_gemv_f16_seg(const uint16_t* w, int nseg, const int* seg_rows,

@@ -34,6 +34,10 @@ SIGNATURES = {
     "rwkvq_gemv_sym": [_P, _P, _P, _P, _I, _I, _I, _I, _P, _L, _P, _I, _I,
                        _P],
     "rwkvq_gemv_rtn8": [_P, _P, _I, _I, _I, _P, _L, _P, _I, _I, _P],
+    "rwkvq_gemv_rtn8_spqr": [_P, _P, _P, _P, _P, _I, _I, _P, _L, _P, _I, _I,
+                             _P],
+    "rwkvq_spqr_apply": [_P, _L, _P, _P, _P, _I, _I, _P, _I, _P],
+    "rwkvq_spqr_scatter": [_P, _P, _P, _I, _P, _L, _P],
     "rwkvq_gemm_sb6": [_P, _P, _P, _I, _I, _I, _I, _P, _L, _P, _I, _I, _P],
     "rwkvq_gemm_sym": [_P, _P, _P, _P, _I, _I, _I, _I, _P, _L, _P, _I, _I,
                        _P],

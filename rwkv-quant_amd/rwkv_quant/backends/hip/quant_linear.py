@@ -288,10 +288,7 @@ class QuantLinearV2(_HipLinearBase):
         self.has_outliers = (qt.outlier_indices is not None
                              and qt.outlier_indices.numel() > 0)
         if self.has_outliers:
-            oi = qt.outlier_indices.long()
-            self._out_rows = oi[:, 0].to(self.device)
-            self._out_cols = oi[:, 1].to(self.device)
-            self._out_vals = qt.outlier_values.float().to(self.device)
+            self.sp_ptr, self.sp_col, self.sp_val = spqr_csr(qt, self.device)
 
     def _kargs(self):
         return "rtn8", (_lib.ptr(self.codes), _lib.ptr(self.scale))
@@ -303,15 +300,29 @@ class QuantLinearV2(_HipLinearBase):
 
     def _run(self, kind, x2, y, out_per=None, mode=_lib.EPI_STORE, n=None,
              x_ld=0):
-        if self.has_outliers and (mode not in (_lib.EPI_STORE, _lib.EPI_ADD)
-                                  or x_ld or out_per):
-            raise NotImplementedError("outliers with a fused epilogue")
-        super()._run(kind, x2, y, out_per, mode, n, x_ld)
-        if self.has_outliers:
-            # codes are 0 at outlier positions; add x[c] * value (linear, so
-            # also right after an accumulate epilogue)
-            y.index_add_(1, self._out_rows,
-                         x2[:, self._out_cols] * self._out_vals)
+        if not self.has_outliers:
+            return super()._run(kind, x2, y, out_per, mode, n, x_ld)
+        if (out_per not in (None, self.out_features) or mode & ~15
+                or mode > _lib.EPI_SIGMOID):
+            raise NotImplementedError("SpQR outliers: one segment, fp32 "
+                                      "x and y")
+        rows = n if n is not None else x2.shape[0]
+        ld = x_ld or self.in_features
+        P = _lib.ptr
+        csr = (P(self.sp_ptr), P(self.sp_col), P(self.sp_val))
+        if kind == "gemv":
+            _lib.call("rwkvq_gemv_rtn8_spqr", P(self.codes), P(self.scale),
+                      *csr, self.out_features, self.in_features, P(x2), ld,
+                      P(y), rows, mode, _lib.stream_handle())
+            return
+        # the MFMA GEMM stores (or accumulates) the int8 part; the outlier
+        # tail and the epilogue follow in rwkvq_spqr_apply (x fp32)
+        add = mode == _lib.EPI_ADD
+        super()._run(kind, x2, y, None, _lib.EPI_ADD if add else
+                     _lib.EPI_STORE, n, x_ld)
+        _lib.call("rwkvq_spqr_apply", P(x2), ld, *csr, self.out_features,
+                  rows, P(y), _lib.EPI_STORE if add else mode,
+                  _lib.stream_handle())
 
     def _f16_args(self):
         if self.has_outliers:
@@ -323,7 +334,27 @@ class QuantLinearV2(_HipLinearBase):
                   _lib.ptr(self.scale), self.out_features, self.in_features,
                   _lib.ptr(w), self.in_features, _lib.stream_handle())
         if self.has_outliers:
-            w[self._out_rows, self._out_cols] = self._out_vals
+            _lib.call("rwkvq_spqr_scatter", _lib.ptr(self.sp_ptr),
+                      _lib.ptr(self.sp_col), _lib.ptr(self.sp_val),
+                      self.out_features, _lib.ptr(w), self.in_features,
+                      _lib.stream_handle())
+
+
+def spqr_csr(qt, device):
+    """The SpQR outliers of an rtn tensor, (row, col) pairs + bf16 values,
+    as CSR per row on the device: row_ptr int32 [rows + 1], cols int32,
+    vals bf16 bits (reference: quant_linear_v2.py:282-321 builds the same
+    row offsets at load)."""
+    rows = int(qt.shape[0])
+    oi = qt.outlier_indices.long().reshape(-1, 2)
+    order = torch.argsort(oi[:, 0] * (1 << 32) + oi[:, 1], stable=True)
+    r, c = oi[order, 0], oi[order, 1]
+    vals = qt.outlier_values.reshape(-1)[order].contiguous().view(torch.int16)
+    counts = torch.bincount(r, minlength=rows)
+    ptr = torch.zeros(rows + 1, dtype=torch.int64, device=oi.device)
+    ptr[1:] = torch.cumsum(counts, 0)
+    to = lambda t, dt: t.to(dtype=dt).to(device).contiguous()
+    return to(ptr, torch.int32), to(c, torch.int32), to(vals, torch.int16)
 
 
 class _FusedBase:

@@ -40,7 +40,7 @@ import torch
 from . import _lib
 from .quant_linear import (GEMM_MIN_BATCH_NB, DenseLinear, GwQuantLinear,
                            GwQuantLinearFused, QuantLinearV2, SymQuantLinear,
-                           SymQuantLinearFused, make_linear)
+                           SymQuantLinearFused, make_linear, spqr_csr)
 
 FUSE = True
 FUSE_DECODE = True
@@ -92,8 +92,9 @@ def dense_param(qt, device):
         _lib.call("rwkvq_dequant_rtn8_f32", _lib.ptr(codes), _lib.ptr(sc),
                   rows, cols, _lib.ptr(out), cols, _stream())
         if qt.outlier_indices is not None and qt.outlier_indices.numel():
-            oi = qt.outlier_indices.long().to(device)
-            out[oi[:, 0], oi[:, 1]] = qt.outlier_values.float().to(device)
+            ptr, col, val = spqr_csr(qt, device)
+            _lib.call("rwkvq_spqr_scatter", _lib.ptr(ptr), _lib.ptr(col),
+                      _lib.ptr(val), rows, _lib.ptr(out), cols, _stream())
     elif qt.gw_mode in ("sb6", "sym") or qt.gw_mode == "":
         lin = make_linear(qt, device)
         lin._dequant_into(out)

@@ -144,3 +144,23 @@ def test_rejects_pickle_container(tmp_path):
         reader.load_raw(p)
     with pytest.raises(ValueError, match="pickle"):
         codec.open_rwkvq(p)
+
+
+def test_spqr_csr_is_the_outlier_set():
+    """The device CSR of the SpQR outliers (built on the CPU here) holds
+    exactly the stored (row, col, value) triples, rows in order."""
+    from rwkv_quant.backends.hip.quant_linear import spqr_csr
+    w = torch.randn(64, 256, generator=torch.Generator().manual_seed(5))
+    c, s, oi, ov = writer.rtn_quantize_outliers(w, 8, 0.02)
+    qt = writer.make_rtn("t", "head", 8, w.shape, c, s, oi, ov)
+    ptr, col, val = spqr_csr(qt, "cpu")
+    ptr, col = ptr.long().numpy(), col.long().numpy()
+    assert ptr[0] == 0 and ptr[-1] == len(col) == oi.shape[0]
+    assert (np.diff(ptr) >= 0).all()
+    rows = np.repeat(np.arange(64), np.diff(ptr))
+    got = {(int(r), int(c_), int(v)) for r, c_, v in
+           zip(rows, col, val.numpy().astype(np.int64))}
+    ref = {(int(r), int(c_), int(v)) for (r, c_), v in
+           zip(oi.long().numpy(), ov.view(torch.int16).numpy()
+               .astype(np.int64))}
+    assert got == ref
