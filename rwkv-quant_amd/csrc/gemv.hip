@@ -27,8 +27,8 @@
 //             rwkv_quant/backends/metal/quant_linear_v2.py:35-84).
 //
 // One or two input rows take this lane-dot kernel; three or more take the
-// matrix-core kernel further down (bgemv_kernel), which multiplies the
-// fp16 weights the format's dequant rounds to, like the prefill GEMM.
+// matrix-core kernel further down (bgemv_kernel), which carries the
+// format's fp32 weights and x each as fp16 hi + lo through the MFMAs.
 #include "qfmt.h"
 #include "rwkvq_hip.h"
 
