@@ -404,6 +404,29 @@ int rwkvq_wkv7_decode_lora(const float* rkv, const float* const* h,
                            float* out, int B, int H, int head_size,
                            void* stream);
 
+/* As rwkvq_wkv7_decode_lora, with the up factors read straight from the
+ * file's codes of a world checkpoint (stored [rank, D], blocks of 64
+ * columns = one head).  Branch k: q[k] the codes permuted to
+ * [H][rank / 16][64][16] (head, 16-row block, channel, row); asym: s[k],
+ * m[k] the fp32 scale / min as [H][rank]; per-row int8 (s[k] null):
+ * sc[k] the fp16 row scales [rank].  Codes, scales and mins enter
+ * exactly; h fp32, the sum fp32 as sum_j q_jc (h_j s_j) + sum_j h_j m_j.
+ * rank[k] % 16 == 0, rank[k] <= 512, sum of ranks <= 1024, q[k]
+ * 16-byte aligned.
+ * Replaces: as rwkvq_wkv7_decode_lora, reading the LoRA codes the file
+ * stores (reference: quant_model.py:462-526, codec.py:260-292). */
+int rwkvq_wkv7_decode_lora_q(const float* rkv, const float* const* h,
+                             const uint8_t* const* q, const float* const* s,
+                             const float* const* m, const uint16_t* const* sc,
+                             const int* rank, const float* w0,
+                             const float* a0, const float* v0,
+                             const float* k_k, const float* k_a,
+                             const float* r_k, const float* ln_w,
+                             const float* ln_b, float* v_first, int layer0,
+                             const float* state_in, float* state_out,
+                             float* out, int B, int H, int head_size,
+                             void* stream);
+
 /* rwkvq_gemm_f16 over up to 8 segments of unequal height (seg_rows[j] a
  * multiple of 128) of one matrix w [sum rows, in]: segment j reads
  * x[t * x_ld + j * in + c] and writes columns [sum_{i<j} rows_i, ...) of
@@ -469,6 +492,26 @@ int rwkvq_lora_gemv(int n_jobs, const void* const* W, const float* const* x,
                     const int* rows, const int* in, const int* epi, int N,
                     void* stream);
 
+
+/* Down products of up to 4 low-rank branches straight from the file's
+ * codes of a world checkpoint (stored [in, rank], blocks along the rank):
+ * y_j[n * y_ld_j + r] = epi_j( sum_c x_j[n * x_ld_j + c] * W_j[r, c] ),
+ * n < N <= 8, with q[j] the codes transposed to [rank, in] and either
+ * asym (s[j], m[j]: fp32 scale / min as [ceil(rank / 64), in]) or
+ * per-row int8 (s[j] null, sc[j]: fp16 scale per input column [in]).
+ * Weights are dequantized exactly as rwkvq_dequant_asym_f32 / _rtn8_f32
+ * give them; x fp32, products and sums fp32.  in in {2048, 2560, 4096},
+ * N * in <= 16384, rank % 16 == 0, x 16-byte aligned with x_ld % 4 == 0,
+ * q 4-byte, s / m 16-byte, sc 8-byte aligned.
+ * Replaces: QuantTMix._lora down products at decode, reading the LoRA
+ * codes the file stores (reference: quant_model.py:462-526,
+ * codec.py:260-292). */
+int rwkvq_lora_down_q(int n_jobs, const uint8_t* const* q,
+                      const float* const* s, const float* const* m,
+                      const uint16_t* const* sc, const float* const* x,
+                      const int* x_ld, float* const* y, const int* y_ld,
+                      const int* rows, const int* epi, int in, int N,
+                      void* stream);
 
 /* ------------------------------------------------------ perplexity
  * nll[r] = logsumexp(logits[r, :V]) - logits[r, target[r]] for r < rows

@@ -458,7 +458,29 @@ struct LoraUp {
 };
 constexpr int kMaxCat = 1024;   // sum of the four ranks
 
-template <bool LORA>
+// The up products straight from the file's codes.  A world checkpoint
+// stores up factor k as [rank, D] with its quantization blocks along D, 64
+// columns = one head: asym (u8 codes, fp32 scale / min per (rank row,
+// head)) or per-row int8 (the g branch: fp16 scale per rank row).  At load
+// the codes are permuted to [H][rank / 16][64][16] (head, 16-row block,
+// channel, row within the block), so lane c of a wave reads the 16 codes
+// of channel c for one row block with one 16-byte load (1 KiB contiguous
+// per wave), and the asym parameters to [H][rank].  The file's codes,
+// scales and mins enter exactly; h stays fp32 and the sum is taken in fp32
+// as sum_j q_jc (h_j s_j) + sum_j h_j m_j (two VALU operations per weight:
+// byte-to-float conversion and a multiply-add).
+struct LoraUpQ {
+  const float* h[4];
+  const uint8_t* q[4];
+  const float* s[4];       // asym scale [H][rank], null for int8
+  const float* m[4];       // asym min [H][rank]
+  const uint16_t* sc[4];   // int8: fp16 scale [rank]
+  int r[4];
+};
+
+// LORA: 0 = branch outputs given (yw, ya, yv, g); 1 = up products from
+// fp16 factors (lu); 2 = up products from the file's codes (lq).
+template <int LORA>
 __global__ void __launch_bounds__(256)
 wkv_decode_k(const float* __restrict__ rkv, const float* __restrict__ yw,
              const float* __restrict__ ya, const float* __restrict__ yv,
@@ -468,7 +490,7 @@ wkv_decode_k(const float* __restrict__ rkv, const float* __restrict__ yw,
              const float* __restrict__ r_k, const float* __restrict__ lnw,
              const float* __restrict__ lnb, float* __restrict__ vfirst,
              int layer0, const float* state_in, float* state_out,
-             float* __restrict__ out, int H, LoraUp lu) {
+             float* __restrict__ out, int H, LoraUp lu, LoraUpQ lq) {
   constexpr int P = 4, C = kHead / P;
   __shared__ float4 s_w[kHead / 4], s_k[kHead / 4], s_a[kHead / 4],
       s_b[kHead / 4], s_r[kHead / 4];
@@ -506,7 +528,137 @@ wkv_decode_k(const float* __restrict__ rkv, const float* __restrict__ yw,
     if (!LORA) { ywe = yw[e]; yae = ya[e]; gc = g[e]; }
   }
   __shared__ float s_up[4][kHead];
-  if constexpr (LORA) {
+  if constexpr (LORA == 2) {
+    // Branch k's output for channel c is
+    //   sum_j h_j (q_jc s_j + m_j) = sum_j q_jc (h_j s_j) + sum_j h_j m_j,
+    // the second term the same for every channel of the head.  int8 codes
+    // are read as unsigned bytes of (q ^ 0x80) = q + 128, their -128 folded
+    // into that term.  Staged per (token, head): hs_j = h_j s_j over the
+    // concatenated rank axis (w, a, v, g; an absent branch has rank 0) and
+    // the per-16-row-block sums of the channel-independent terms.
+    __shared__ float4 s_hs4[kMaxCat / 4];
+    __shared__ float s_cj[kMaxCat];
+    __shared__ float s_bm[kMaxCat / 16];
+    __shared__ float s_red[4][4][kHead];
+    float* s_hs = reinterpret_cast<float*>(s_hs4);
+    const int r0 = lq.r[0], r1 = lq.r[1], r2 = lq.r[2], r3 = lq.r[3];
+    const int o1 = r0, o2 = o1 + r1, o3 = o2 + r2, R = o3 + r3;
+    // each selection below indexes the argument table with constants (a
+    // dynamic index would copy it to scratch)
+    auto br = [&](int p) { return p < o1 ? 0 : p < o2 ? 1 : p < o3 ? 2 : 3; };
+    auto off = [&](int k) { return k == 0 ? 0 : k == 1 ? o1 : k == 2 ? o2 : o3; };
+    auto rk_of = [&](int k) { return k == 0 ? r0 : k == 1 ? r1 : k == 2 ? r2 : r3; };
+    auto s_of = [&](int k) { return k == 0 ? lq.s[0] : k == 1 ? lq.s[1]
+                                  : k == 2 ? lq.s[2] : lq.s[3]; };
+    const int cl = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nb = R >> 4;
+    // code blocks of this wave (blocks wv, wv + 4, ...), loads first
+    uint4 cv[kMaxCat / 64];
+#pragma unroll
+    for (int i = 0; i < kMaxCat / 64; ++i) {
+      const int b = wv + 4 * i;
+      if (b < nb) {
+        const int k = br(16 * b);
+        const uint8_t* qk = k == 0 ? lq.q[0] : k == 1 ? lq.q[1]
+                          : k == 2 ? lq.q[2] : lq.q[3];
+        const int rk = rk_of(k), lb = (16 * b - off(k)) >> 4;
+        cv[i] = ld16(qk + (((size_t)h * (rk >> 4) + lb) * kHead + cl) * 16);
+      }
+    }
+    // h and the block parameters, branch by branch (pointers and formats
+    // are then uniform), rank positions j = tid, tid + 256 (rank <= 512,
+    // clamped into the branch for the loads); raw bits first, every load
+    // in flight before the first use
+    uint32_t hraw[4][2], sraw[4][2], mraw[4][2], craw[4][2];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int rk = lq.r[k];
+      if (rk == 0) continue;
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int j = min(tid + 256 * t, rk - 1);
+        hraw[k][t] = __float_as_uint(lq.h[k][(size_t)bi * rk + j]);
+        if (lq.s[k]) {
+          sraw[k][t] = __float_as_uint(lq.s[k][(size_t)h * rk + j]);
+          mraw[k][t] = __float_as_uint(lq.m[k][(size_t)h * rk + j]);
+        } else {
+          craw[k][t] = lq.sc[k][j];
+        }
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int rk = lq.r[k], o = k == 0 ? 0 : k == 1 ? o1 : k == 2 ? o2 : o3;
+      if (rk == 0) continue;
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int j = tid + 256 * t;
+        if (j < rk) {
+          pin(hraw[k][t]);
+          const float hv = __uint_as_float(hraw[k][t]);
+          if (lq.s[k]) {
+            pin(sraw[k][t]);
+            pin(mraw[k][t]);
+            const float hs = hv * __uint_as_float(sraw[k][t]);
+            s_hs[o + j] = hs;
+            s_cj[o + j] = hv * __uint_as_float(mraw[k][t]);
+          } else {
+            pin(craw[k][t]);
+            const float hs = hv * f16_bits_to_f32(craw[k][t]);
+            s_hs[o + j] = hs;
+            s_cj[o + j] = -128.f * hs;
+          }
+        }
+      }
+    }
+    __syncthreads();
+    if (tid < nb) {                            // fixed-order block sums
+      float a = 0.f;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) a += s_cj[16 * tid + e];
+      s_bm[tid] = a;
+    }
+    __syncthreads();
+    // each block's channel-independent sum joins the accumulator of the
+    // wave that takes the block, so the four waves' partials add up to it
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < kMaxCat / 64; ++i) {
+      const int b = wv + 4 * i;
+      if (b < nb) {
+        const int k = br(16 * b);
+        const uint32_t flip = s_of(k) ? 0u : 0x80808080u;
+        const uint32_t wd[4] = {cv[i].x ^ flip, cv[i].y ^ flip,
+                                cv[i].z ^ flip, cv[i].w ^ flip};
+        float d0 = 0.f, d1 = 0.f;
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) {
+          const float4 hs = s_hs4[4 * b + qd];
+          const uint32_t w = wd[qd];
+          d0 = fmaf((float)(w & 0xFFu), hs.x, d0);
+          d1 = fmaf((float)((w >> 8) & 0xFFu), hs.y, d1);
+          d0 = fmaf((float)((w >> 16) & 0xFFu), hs.z, d0);
+          d1 = fmaf((float)(w >> 24), hs.w, d1);
+        }
+        const float d = (d0 + d1) + s_bm[b];
+        if (k == 0) acc[0] += d;
+        else if (k == 1) acc[1] += d;
+        else if (k == 2) acc[2] += d;
+        else acc[3] += d;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) s_red[wv][k][cl] = acc[k];
+    __syncthreads();
+    if (tid < kHead) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        s_up[k][tid] = (s_red[0][k][tid] + s_red[1][k][tid]) +
+                       (s_red[2][k][tid] + s_red[3][k][tid]);
+    }
+  } else if constexpr (LORA == 1) {
     // The four branches' down outputs of token bi, concatenated (w, a, v,
     // g; an absent branch has rank 0) as fp16 pairs (the reference rounds
     // the low-rank activations to fp16 before the up product).
@@ -1294,11 +1446,11 @@ int rwkvq_wkv7_decode(const float* rkv, const float* yw, const float* ya,
                       int B, int H, int head_size, void* stream) {
   if (B <= 0 || H <= 0 || head_size != kHead || (!layer0 && (!yv || !v0)))
     return RWKVQ_ERR_ARG;
-  hipLaunchKernelGGL(wkv_decode_k<false>, dim3(B * H), dim3(256), 0,
+  hipLaunchKernelGGL(wkv_decode_k<0>, dim3(B * H), dim3(256), 0,
                      (hipStream_t)stream, rkv, yw, ya, yv, g, w0, a0, v0, k_k,
                      k_a, r_k, ln_w, ln_b, v_first, layer0,
                      state_in ? state_in : state_out, state_out, out, H,
-                     LoraUp{});
+                     LoraUp{}, LoraUpQ{});
   return ok_launch();
 }
 
@@ -1324,11 +1476,48 @@ int rwkvq_wkv7_decode_lora(const float* rkv, const float* const* h,
   }
   if (!layer0 && !v0) return RWKVQ_ERR_ARG;
   if (lu.r[0] + lu.r[1] + lu.r[2] + lu.r[3] > kMaxCat) return RWKVQ_ERR_SIZE;
-  hipLaunchKernelGGL(wkv_decode_k<true>, dim3(B * H), dim3(256), 0,
+  hipLaunchKernelGGL(wkv_decode_k<1>, dim3(B * H), dim3(256), 0,
                      (hipStream_t)stream, rkv, nullptr, nullptr, nullptr,
                      nullptr, w0, a0, v0, k_k, k_a, r_k, ln_w, ln_b, v_first,
                      layer0, state_in ? state_in : state_out, state_out, out,
-                     H, lu);
+                     H, lu, LoraUpQ{});
+  return ok_launch();
+}
+
+int rwkvq_wkv7_decode_lora_q(const float* rkv, const float* const* h,
+                             const uint8_t* const* q, const float* const* s,
+                             const float* const* m, const uint16_t* const* sc,
+                             const int* rank, const float* w0,
+                             const float* a0, const float* v0,
+                             const float* k_k, const float* k_a,
+                             const float* r_k, const float* ln_w,
+                             const float* ln_b, float* v_first, int layer0,
+                             const float* state_in, float* state_out,
+                             float* out, int B, int H, int head_size,
+                             void* stream) {
+  if (B <= 0 || H <= 0 || head_size != kHead) return RWKVQ_ERR_ARG;
+  LoraUpQ lq{};
+  for (int k = 0; k < 4; ++k) {
+    const bool need = k != 2 || !layer0;       // no v branch in layer 0
+    if (!need) continue;
+    const bool i8 = s[k] == nullptr;
+    if (!h[k] || !q[k] || rank[k] <= 0 || rank[k] % 16 || rank[k] > 512 ||
+        (i8 ? !sc[k] : !m[k]) || (reinterpret_cast<uintptr_t>(q[k]) & 15))
+      return RWKVQ_ERR_ARG;
+    lq.h[k] = h[k];
+    lq.q[k] = q[k];
+    lq.s[k] = s[k];
+    lq.m[k] = i8 ? nullptr : m[k];
+    lq.sc[k] = i8 ? sc[k] : nullptr;
+    lq.r[k] = rank[k];
+  }
+  if (!layer0 && !v0) return RWKVQ_ERR_ARG;
+  if (lq.r[0] + lq.r[1] + lq.r[2] + lq.r[3] > kMaxCat) return RWKVQ_ERR_SIZE;
+  hipLaunchKernelGGL(wkv_decode_k<2>, dim3(B * H), dim3(256), 0,
+                     (hipStream_t)stream, rkv, nullptr, nullptr, nullptr,
+                     nullptr, w0, a0, v0, k_k, k_a, r_k, ln_w, ln_b, v_first,
+                     layer0, state_in ? state_in : state_out, state_out, out,
+                     H, LoraUp{}, lq);
   return ok_launch();
 }
 

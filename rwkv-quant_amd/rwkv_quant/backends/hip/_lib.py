@@ -83,6 +83,11 @@ SIGNATURES = {
                                _P, _P, _I, _P, _P, _P, _I, _I, _I, _P],
     "rwkvq_wkv7_decode": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                           _P, _P, _I, _P, _P, _P, _I, _I, _I, _P],
+    "rwkvq_lora_down_q": [_I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I,
+                          _P],
+    "rwkvq_wkv7_decode_lora_q": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                 _P, _P, _P, _P, _P, _I, _P, _P, _P, _I, _I,
+                                 _I, _P],
 }
 
 _lib = None

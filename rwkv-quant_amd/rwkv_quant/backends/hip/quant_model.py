@@ -21,7 +21,9 @@ Execution per layer (every numeric step is a librwkvq_hip kernel):
   wkv_prep -> wkv7_scan -> wkv_tail -> o_proj GEMV (+= residual) ->
   shift_lerp(ln2, 1 lerp) -> key GEMV (relu^2) -> value GEMV (+= residual)
 Decode (T = 1) runs LoRA up + prep + one recurrence step + tail as one
-launch per (sequence, head).
+launch per (sequence, head).  On a world checkpoint the decode LoRA reads
+the file's codes (asym gw64 / per-row int8, exact weights) instead of the
+fp16 copies the prefill GEMMs use.
 Prefill (B*T >= GEMM_MIN_BATCH_NB) runs the projections on the MFMA GEMM
 kernel (dequantization fused into the operand load, epilogue fused, the
 r/k/v triple in one launch) and the LoRA products as fp16 GEMMs.
@@ -31,6 +33,7 @@ Runtime switches (module attributes, as the reference's FUSE flags):
   FUSE_DECODE decode (T = 1): the LoRA up products folded into the WKV
               step (one launch fewer per layer)
   USE_GRAPH   replay decode steps from a captured HIP graph
+  LORA_FROM_CODES  decode LoRA from the file's codes (world checkpoints)
 """
 import ctypes
 from collections import OrderedDict
@@ -41,6 +44,7 @@ from . import _lib
 from .quant_linear import (GEMM_MIN_BATCH_NB, DenseLinear, GwQuantLinear,
                            GwQuantLinearFused, QuantLinearV2, SymQuantLinear,
                            SymQuantLinearFused, make_linear, spqr_csr)
+from .repack import lora_codes_ok, lora_down_device, lora_up_device
 
 FUSE = True
 FUSE_DECODE = True
@@ -57,6 +61,11 @@ WKV_PREP_FUSED = True          # chunked prefill: per-channel prep inside the
 X16_PREFILL = True             # prefill GEMM inputs written as fp16 in the
                                # GEMM's pair order by their producers
 LORA_GEMV_ROWS = 32            # decode-batch rows per LoRA-down GEMV launch
+LORA_FROM_CODES = True         # decode LoRA (world checkpoints) read from
+                               # the file's codes instead of fp16 copies
+                               # (checked at run time, like FUSE_DECODE)
+LORA_Q_MAX_NC = 16384          # rows x width the code-based down kernel
+                               # stages in LDS (64 KiB of fp32 x)
 MAX_SEQ_GRAPHS = 8             # captured forward_stateful graphs kept (LRU);
                                # each owns its logits and two state sets
 
@@ -205,6 +214,35 @@ def wkv_ops_floats(N, H):
     return max(1, slots * H * WKV_CHUNK_OPS)
 
 
+def _lora_codes(g, branches, C, head_size, device):
+    """Device layouts of the decode LoRA factors read straight from the
+    file's codes (world checkpoint: down stored [C, rank], up [rank, C]);
+    None when a factor's format or shape does not allow it."""
+    if head_size != 64 or C not in (2048, 2560, 4096):
+        return None
+    on = lambda a: None if a is None else torch.from_numpy(a).to(device)
+    cpu = lambda t: None if t is None else t.detach().cpu().numpy()
+    out = {}
+    for b in branches:
+        dq, uq = g(b + "1"), g(b + "2")
+        if not (lora_codes_ok(dq, 1, lambda c: c % 16 == 0)
+                and dq.shape[0] == C
+                and lora_codes_ok(uq, 16, lambda c: c == C)
+                and uq.shape[0] == dq.shape[1]):
+            return None
+        lays = []
+        for qt, fn in ((dq, lora_down_device), (uq, lora_up_device)):
+            if qt.gw_mode == "asym":
+                lay = fn(cpu(qt.codes), tuple(qt.shape), scale=cpu(qt.gw_scale),
+                         mn=cpu(qt.gw_min))
+            else:
+                lay = fn(cpu(qt.codes), tuple(qt.shape),
+                         row_scale=cpu(qt.scale))
+            lays.append({k: on(v) for k, v in lay.items()})
+        out[b] = (dq.shape[1], lays[0], lays[1])
+    return out
+
+
 class QuantTMix:
     def __init__(self, tensors, prefix, naming, layer_id, n_head, head_size,
                  device):
@@ -280,6 +318,11 @@ class QuantTMix:
                 all(lins[0].can_fuse_with(l) for l in lins):
             self.rkv_fused = SymQuantLinearFused(lins)
 
+        # decode LoRA straight from the file's codes (world checkpoints)
+        self.lora_q = None
+        if naming == "world":
+            self.lora_q = _lora_codes(lambda nm: g(pre + nm), list(self.lora),
+                                      C, head_size, dev)
         # decode fusion (LoRA up into the WKV step) needs ranks the fused
         # WKV kernel tiles
         self.decode_fusable = (
@@ -454,6 +497,24 @@ class QuantTMix:
         the stacked factors; fewer: the grouped lane-dot kernel."""
         N, C = wk.N, self.C
         xs_flat = wk.xs.view(N, 6 * C)
+        if (LORA_FROM_CODES and self.lora_q is not None
+                and N * C <= LORA_Q_MAX_NC):
+            br = list(self.lora_q)
+            n = len(br)
+            P = ctypes.c_void_p
+            lay = [self.lora_q[b][1] for b in br]
+            pa = lambda key: (P * n)(*[None if l[key] is None
+                                       else l[key].data_ptr() for l in lay])
+            ia = lambda v: (ctypes.c_int * n)(*v)
+            _lib.call("rwkvq_lora_down_q", n, pa("q"), pa("s"), pa("m"),
+                      pa("sc"),
+                      (P * n)(*[xs_flat[:, self.SLOT[b] * C:].data_ptr()
+                                for b in br]),
+                      ia([6 * C] * n), (P * n)(*[wk.h[b].data_ptr() for b in br]),
+                      ia([wk.h[b].shape[1] for b in br]),
+                      ia([self.lora_q[b][0] for b in br]),
+                      ia([self.EPI_DOWN[b] for b in br]), C, N, _stream())
+            return
         if N >= DOWN_SEG_MIN_N and self.down_seg_ok and N <= 16:
             order = self.down_order
             rows = (ctypes.c_int * len(order))(
@@ -478,6 +539,25 @@ class QuantTMix:
         """Decode WKV step with the LoRA up products folded in."""
         order = ("w", "a", "v", "g")
         have = [b in self.lora for b in order]
+        if LORA_FROM_CODES and self.lora_q is not None:
+            P = ctypes.c_void_p
+            ups = [self.lora_q[b][2] if h else None
+                   for b, h in zip(order, have)]
+            pa = lambda key: (P * 4)(*[None if u is None or u[key] is None
+                                       else u[key].data_ptr() for u in ups])
+            _lib.call("rwkvq_wkv7_decode_lora_q", _lib.ptr(wk.rkv),
+                      (P * 4)(*[wk.h[b].data_ptr() if h else None
+                                for b, h in zip(order, have)]),
+                      pa("q"), pa("s"), pa("m"), pa("sc"),
+                      (ctypes.c_int * 4)(*[self.lora_q[b][0] if h else 0
+                                           for b, h in zip(order, have)]),
+                      _lib.ptr(self.w0), _lib.ptr(self.a0), _lib.ptr(self.v0),
+                      _lib.ptr(self.k_k), _lib.ptr(self.k_a),
+                      _lib.ptr(self.r_k), _lib.ptr(self.ln_x_w),
+                      _lib.ptr(self.ln_x_b), _lib.ptr(wk.v_first), layer0,
+                      _lib.ptr(wkv_in), _lib.ptr(wkv_out), _lib.ptr(wk.o), B,
+                      H, S, _stream())
+            return
         hp = (ctypes.c_void_p * 4)(*[wk.h[b].data_ptr() if h else None
                                      for b, h in zip(order, have)])
         bp = (ctypes.c_void_p * 4)(*[self.lora[b][1].data_ptr() if h

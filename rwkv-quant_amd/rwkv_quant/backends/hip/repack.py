@@ -14,6 +14,13 @@ same byte count (nothing is recomputed, no scale is widened):
   sym    codes / codes_packed unchanged, hb crumbs as above with the
          16-wide block pairing, gw_qs and gw_d unchanged
   rtn@8  unchanged (scale flattened to [rows])
+  LoRA factors of a world checkpoint, read by the decode kernels straight
+  from their codes (asym gw64 or per-row int8; stored [in, out]):
+    down [in, rank]  codes transposed to [rank, in]; asym scale / min to
+                     [rank / 64, in]; int8 row scales [in] unchanged
+    up   [rank, D]   codes permuted to [D / 64][rank / 16][64][16] (head,
+                     16-row block, channel, row); asym scale / min to
+                     [D / 64, rank]; int8 row scales [rank] unchanged
 
 The reference loader performs the analogous interleave for its Metal
 kernels (reference: rwkv_quant/formats/codec.py:407-435,
@@ -98,3 +105,54 @@ def rtn8_device(codes, scale, *, shape):
                                           .reshape(n_out, n_in)),
             "scale": np.ascontiguousarray(np.asarray(scale, np.float16)
                                           .reshape(n_out))}
+
+
+def lora_codes_ok(qt, rows_mult, cols_ok):
+    """True when the decode kernels can read this LoRA factor's codes:
+    asym with 64-column blocks, or per-row int8 without outliers."""
+    if len(qt.shape) != 2 or qt.codes is None:
+        return False
+    r, c = qt.shape
+    if r % rows_mult or not cols_ok(c):
+        return False
+    if qt.gw_mode == "asym":
+        return qt.gw_gs == 64 and qt.bits <= 8
+    return (qt.gw_mode == "" and qt.bits == 8 and
+            (qt.outlier_indices is None or qt.outlier_indices.numel() == 0))
+
+
+def lora_down_device(codes, shape, *, scale=None, mn=None, row_scale=None):
+    """Down factor stored [in, rank]: asym (scale / min [in, rank / 64])
+    or per-row int8 (row_scale [in])."""
+    n_in, rank = shape
+    q = np.asarray(codes).view(np.uint8).reshape(n_in, rank)
+    out = {"q": np.ascontiguousarray(q.T), "s": None, "m": None, "sc": None}
+    if scale is not None:
+        nb = -(-rank // 64)
+        out["s"] = np.ascontiguousarray(
+            np.asarray(scale, np.float32).reshape(n_in, nb).T)
+        out["m"] = np.ascontiguousarray(
+            np.asarray(mn, np.float32).reshape(n_in, nb).T)
+    else:
+        out["sc"] = np.ascontiguousarray(
+            np.asarray(row_scale, np.float16).reshape(n_in).view(np.uint16))
+    return out
+
+
+def lora_up_device(codes, shape, *, scale=None, mn=None, row_scale=None):
+    """Up factor stored [rank, D] (64-column blocks = heads): asym
+    (scale / min [rank, D / 64]) or per-row int8 (row_scale [rank])."""
+    rank, d = shape
+    H = d // 64
+    q = np.asarray(codes).view(np.uint8).reshape(rank // 16, 16, H, 64)
+    out = {"q": np.ascontiguousarray(q.transpose(2, 0, 3, 1)),
+           "s": None, "m": None, "sc": None}
+    if scale is not None:
+        out["s"] = np.ascontiguousarray(
+            np.asarray(scale, np.float32).reshape(rank, H).T)
+        out["m"] = np.ascontiguousarray(
+            np.asarray(mn, np.float32).reshape(rank, H).T)
+    else:
+        out["sc"] = np.ascontiguousarray(
+            np.asarray(row_scale, np.float16).reshape(rank).view(np.uint16))
+    return out
