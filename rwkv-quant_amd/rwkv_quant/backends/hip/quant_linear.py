@@ -22,6 +22,8 @@ into its operand load and fp16 operands, as the reference's prefill
 matmul.  Every path runs a HIP kernel of librwkvq_hip; nothing here
 computes on the CPU.
 """
+import ctypes
+
 import numpy as np
 import torch
 
@@ -102,20 +104,10 @@ class _HipLinearBase:
         elif self.gemm_ok(out_per):
             self._run("gemm", x2, y, out_per, mode, n, x_ld)
         else:
-            if out_per:
-                raise NotImplementedError("segmented input off the MFMA tiles")
-            if x_ld:
-                x2 = torch.as_strided(x2, (rows, self.in_features), (x_ld, 1))
-            out = self._gemm_dense(x2.contiguous(), _lib.EPI_STORE)
-            if mode == _lib.EPI_STORE:
-                y.copy_(out)
-            elif mode == _lib.EPI_ADD:
-                y.add_(out)
-            elif mode == _lib.EPI_RELU2:
-                y.copy_(torch.relu(out))
-                y.mul_(y)
-            else:
-                raise NotImplementedError(mode)
+            # output rows off the MFMA GEMM's 128-row tiles: the GEMV
+            # kernels take any number of input rows (in launches of up to
+            # 32), exact weights and fp32 x
+            self._gemv(x2, y, out_per, mode, n, x_ld)
 
     def __call__(self, x, mode=_lib.EPI_STORE):
         lead, x2 = _flat_x(x, self.in_features)
@@ -137,15 +129,6 @@ class _HipLinearBase:
         GEMM_MIN_BATCH_NB rows, the MFMA GEMM from there on."""
         self._apply(x2, y, mode=mode, n=n, x_ld=x_ld)
         return y
-
-    def _gemm_dense(self, x2, mode):
-        # shapes the MFMA tiles do not cover: dense fp16 weights from the
-        # dequant kernel and an fp16 matmul with fp32 output, the
-        # reference's own prefill path (reference: quant_linear_gw.py:846-849)
-        if mode != _lib.EPI_STORE:
-            raise NotImplementedError("dense GEMM path: store epilogue only")
-        w = self._dequant_w(torch.float16)
-        return torch.matmul(x2.half(), w.t()).float()
 
     def _dequant_w(self, dtype=torch.float16):
         """Dense [OUT, IN]; float32 is bit-exact with the format's dequant,
@@ -444,14 +427,43 @@ def make_linear(qt, device="cuda"):
 
 
 class DenseLinear:
-    """Unquantized [out, in] weight kept in fp16 (reference: quant_model.py:202-210)."""
+    """Unquantized [out, in] weight kept in fp16 (reference:
+    quant_model.py:202-210), multiplied by the fp16 kernels of librwkvq_hip:
+    below GEMM_MIN_BATCH_NB input rows the matrix-core GEMV
+    (rwkvq_gemv_f16_seg, up to 32 rows per launch; fp32 x carried as fp16
+    hi + lo), from there the MFMA GEMM (rwkvq_gemm_f16_seg, fp16 x, as the
+    reference's fp16 matmul).  in % 128 == 0 and out % 16 == 0 (the GEMM
+    also out % 128); other shapes raise at construction."""
 
     def __init__(self, w, device="cuda"):
         self.w = w.to(device=device, dtype=torch.float16).contiguous()
         self.out_features, self.in_features = self.w.shape
         self.device = self.w.device
+        if self.in_features % 128 or self.out_features % 16:
+            raise NotImplementedError(
+                f"fp16 linear {tuple(self.w.shape)}: needs in % 128 == 0 and "
+                f"out % 16 == 0")
+
+    def apply_into(self, x2, y, mode=_lib.EPI_STORE, n=None, x_ld=0):
+        rows = n if n is not None else x2.shape[0]
+        ld = x_ld or self.in_features
+        rows_arr = (ctypes.c_int * 1)(self.out_features)
+        if rows >= GEMM_MIN_BATCH_NB and self.out_features % GEMM_ROW_TILE == 0:
+            _lib.call("rwkvq_gemm_f16_seg", _lib.ptr(self.w), 1, rows_arr,
+                      self.in_features, _lib.ptr(x2), ld, _lib.ptr(y), rows,
+                      mode, 0, _lib.stream_handle())
+            return y
+        for n0 in range(0, rows, 32):
+            nn = min(32, rows - n0)
+            ys = (ctypes.c_void_p * 1)(y.data_ptr() + 4 * n0 * self.out_features)
+            _lib.call("rwkvq_gemv_f16_seg", _lib.ptr(self.w), 1, rows_arr,
+                      self.in_features, x2.data_ptr() + 4 * n0 * ld, ld, ys,
+                      nn, mode, _lib.stream_handle())
+        return y
 
     def __call__(self, x, mode=_lib.EPI_STORE):
         lead, x2 = _flat_x(x, self.in_features)
-        y = torch.matmul(x2.half(), self.w.t()).float()
+        y = torch.empty((x2.shape[0], self.out_features), dtype=torch.float32,
+                        device=x2.device)
+        self.apply_into(x2, y, mode=mode)
         return y.reshape(*lead, self.out_features)

@@ -41,7 +41,7 @@ from collections import OrderedDict
 import torch
 
 from . import _lib
-from .quant_linear import (GEMM_MIN_BATCH_NB, DenseLinear, GwQuantLinear,
+from .quant_linear import (GEMM_MIN_BATCH_NB, GwQuantLinear,
                            GwQuantLinearFused, QuantLinearV2, SymQuantLinear,
                            SymQuantLinearFused, make_linear, spqr_csr)
 from .repack import lora_codes_ok, lora_down_device, lora_up_device
@@ -640,22 +640,7 @@ def _x16_orders(blk):
 def _apply(lin, x2, y, mode, n=None, x_ld=0):
     """y <- epi(x2 @ W^T): GEMV kernel for small N, MFMA GEMM for prefill
     (both with the epilogue fused)."""
-    if not isinstance(lin, DenseLinear):
-        return lin.apply_into(x2, y, mode=mode, n=n, x_ld=x_ld)
-    N = n if n is not None else x2.shape[0]
-    if x_ld:
-        x2 = torch.as_strided(x2, (N, lin.in_features), (x_ld, 1))
-    out = lin(x2)
-    if mode == _lib.EPI_STORE:
-        y.copy_(out)
-    elif mode == _lib.EPI_ADD:
-        y.add_(out)
-    elif mode == _lib.EPI_RELU2:
-        y.copy_(torch.relu(out))
-        y.mul_(y)
-    else:
-        raise NotImplementedError(mode)
-    return y
+    return lin.apply_into(x2, y, mode=mode, n=n, x_ld=x_ld)
 
 
 class QuantRWKV7:
