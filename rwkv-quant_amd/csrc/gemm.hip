@@ -41,6 +41,10 @@
 
 using namespace rwkvq;
 
+#ifndef RWKVQ_GEMM_BX_PIN
+#define RWKVQ_GEMM_BX_PIN 1
+#endif
+
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
@@ -350,6 +354,11 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a0, const int bid,
     for (int k = 0; k < 8; ++k) {
       const int gi = k >> 2, ss = k & 3;
       if (k + 1 < 8) read_bx(k + 1, bx[(k + 1) & 1]);
+#if RWKVQ_GEMM_BX_PIN
+      // the next round's x reads stay ahead of this round's MFMAs (left to
+      // itself the scheduler sinks them next to their use)
+      __builtin_amdgcn_sched_barrier(0);
+#endif
       if (k == 1) {
 #pragma unroll
         for (int ni = 0; ni < WN; ++ni)
@@ -617,7 +626,10 @@ gemm_dual_kernel(GemmArgs a, GemmArgs b, int grid_a) {
 #define RWKVQ_SPLIT_WGS 192
 #endif
 constexpr int kMinRun = 8;
-constexpr int kLongRun = 32;
+#ifndef RWKVQ_GEMM_LONG_RUN
+#define RWKVQ_GEMM_LONG_RUN 32
+#endif
+constexpr int kLongRun = RWKVQ_GEMM_LONG_RUN;
 
 // Split-K workspace registered by the caller (rwkvq_gemm_workspace), one
 // per device.
