@@ -18,7 +18,10 @@
 // lo pair of x * 2^e (a power of two per group, so no fp16 range limit):
 // two v_dot2_f32_f16 per code pair multiply the codes by hi and by lo with
 // exact products and fp32 sums, so the block sums carry x to about 22 bits
-// (fp32 x within the fp32 rounding of the sums).  Block scales follow the
+// (fp32 x within the fp32 rounding of the sums).  The int8 formats (rtn8,
+// sym8) take x instead as three int8 digits under the group's power of two
+// (about 21 bits) and multiply the stored codes directly with exact int32
+// v_dot4_i32_i8 (no decode: head 29.6 -> 28.3 us).  Block scales follow the
 // format: s = f32(f16(qs * d)) (sb6 also m = f32(f16(qm * dm)), s clamped at
 // 1e-8), identical to the reference arithmetic
 // (reference: rwkv_quant/formats/codec.py:183-257,
@@ -72,13 +75,84 @@ struct GemvArgs {
   const uint16_t* sp_val;
 };
 
+#ifndef RWKVQ_GEMV_I8DOT
+#define RWKVQ_GEMV_I8DOT 1
+#endif
+// int8 codes (rtn8, sym8) take x as three int8 digits instead of fp16
+// hi + lo: the code products are then exact int32 dot products
+// (v_dot4_i32_i8, four columns per instruction, no decode of the codes).
+template <int FMT>
+constexpr bool kI8 = RWKVQ_GEMV_I8DOT && (FMT == F_RTN8 || FMT == F_SYM8);
+
+// Power of two for the int8 digits of a group whose largest |x| is amax:
+// amax 2^e in [63.75, 127.5), so the first digit fits [-127, 127].
+__device__ __forceinline__ int digit_exp(float amax) {
+  if (!(amax > 0.f)) return 0;
+  int e = 6 - ilogbf(amax);
+  if (ldexpf(amax, e) >= 127.5f) --e;
+  return min(e, 126);
+}
+
+// Digits of one value: x 2^e = d0 + d1 / 128 + d2 / 16384 + r, |r| <= 2^-15
+// (each step exact in fp32), d0 in [-127, 127], d1 and d2 in [-64, 64];
+// relative to the group's largest |x| about 21 bits.  Returned as bytes.
+__device__ __forceinline__ void x_digit3(float x, int e, uint32_t& b0,
+                                         uint32_t& b1, uint32_t& b2) {
+  const float a = ldexpf(x, e);
+  const float d0 = rintf(a);
+  const float r1 = (a - d0) * 128.f;
+  const float d1 = rintf(r1);
+  const float d2 = rintf((r1 - d1) * 128.f);
+  b0 = (uint32_t)(int)d0 & 0xFFu;
+  b1 = (uint32_t)(int)d1 & 0xFFu;
+  b2 = (uint32_t)(int)d2 & 0xFFu;
+}
+
+// One lane's 32 values of a group as digit words: w[0..7] first digits,
+// w[8..15] second, w[16..23] third (bytes in column order, word k = columns
+// 4k..4k+3); isc = 2^-e, NaN when the group holds a non-finite x (the
+// result is then NaN rather than a finite number).
+__device__ __forceinline__ void x_digits(const float xv[32], uint32_t w[24],
+                                         float& isc) {
+  float amax = 0.f;
+  bool bad = false;
+#pragma unroll
+  for (int c = 0; c < 32; ++c) {
+    amax = fmaxf(amax, fabsf(xv[c]));
+    bad |= !(fabsf(xv[c]) <= 3.4e38f);
+  }
+  const int e = digit_exp(amax);
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    uint32_t w0 = 0u, w1 = 0u, w2 = 0u;
+#pragma unroll
+    for (int bb = 0; bb < 4; ++bb) {
+      uint32_t b0, b1, b2;
+      x_digit3(bad ? 0.f : xv[4 * k + bb], e, b0, b1, b2);
+      w0 |= b0 << (8 * bb);
+      w1 |= b1 << (8 * bb);
+      w2 |= b2 << (8 * bb);
+    }
+    w[k] = w0;
+    w[8 + k] = w1;
+    w[16 + k] = w2;
+  }
+  isc = bad ? __builtin_nanf("") : ldexpf(1.f, -e);
+}
+
+// Sum of the three digit dot products, unscaled: s0 + s1 / 128 + s2 / 16384.
+__device__ __forceinline__ float digit_sum(int s0, int s1, int s2) {
+  return fmaf(fmaf((float)s2, 0.0078125f, (float)s1), 0.0078125f, (float)s0);
+}
+
 // Convert one lane's 32 x values of group g into the format's pair order
 // as an fp16 hi + lo split of x * 2^e: hi = f16(x 2^e), lo = f16(x 2^e - hi),
 // so hi + lo holds x to about 22 bits.  The power of two 2^e (exact) puts
 // the group's largest |x| in [2^14, 2^15): no fp16 overflow whatever the
 // range of x, and lo stays a normal fp16 down to 2^-17 of that maximum.
 // dst: 16 hi pairs, then 16 lo pairs; sums: the fp32 sum of x (the sb6
-// min term) and 2^-e.
+// min term) and 2^-e.  int8 formats: the digit words of x_digits instead
+// (hi = first and second digits, lo[0..7] = third).
 template <int FMT>
 __device__ __forceinline__ void x_group_regs(const float* __restrict__ xp,
                                              uint32_t hi[16], uint32_t lo[16],
@@ -89,6 +163,16 @@ __device__ __forceinline__ void x_group_regs(const float* __restrict__ xp,
     float4 f = reinterpret_cast<const float4*>(xp)[t];
     xv[4 * t] = f.x; xv[4 * t + 1] = f.y; xv[4 * t + 2] = f.z;
     xv[4 * t + 3] = f.w;
+  }
+  if constexpr (kI8<FMT>) {
+    uint32_t w[24];
+    x_digits(xv, w, isc);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) hi[i] = w[i];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) { lo[i] = w[16 + i]; lo[8 + i] = 0u; }
+    sum = 0.f;
+    return;
   }
   float amax = 0.f, sf = 0.f;
 #pragma unroll
@@ -210,6 +294,46 @@ gemv_kernel(GemvArgs a) {
     }
   }
   } else {
+  if constexpr (kI8<FMT>) {
+    // digits: 8 threads per (input row, group), 4 columns each; the
+    // group's largest |x| through three butterflies over those 8 lanes
+    for (int it = threadIdx.x; it < NN * ng * 8; it += blockDim.x) {
+      const int item = it >> 3, k = it & 7;
+      const int n = item / ng, gg = item % ng;
+      float4 f = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (n < a.n)
+        f = reinterpret_cast<const float4*>(
+            a.x + (size_t)n * a.x_ld + (size_t)seg * a.in + (size_t)gg * 32)[k];
+      const float xv4[4] = {f.x, f.y, f.z, f.w};
+      float amax = fmaxf(fmaxf(fabsf(f.x), fabsf(f.y)),
+                         fmaxf(fabsf(f.z), fabsf(f.w)));
+      int bad = !(fabsf(f.x) <= 3.4e38f) | !(fabsf(f.y) <= 3.4e38f) |
+                !(fabsf(f.z) <= 3.4e38f) | !(fabsf(f.w) <= 3.4e38f);
+#pragma unroll
+      for (int m = 1; m < 8; m <<= 1) {
+        amax = fmaxf(amax, __shfl_xor(amax, m, 64));
+        bad |= __shfl_xor(bad, m, 64);
+      }
+      const int e = digit_exp(amax);
+      uint32_t w0 = 0u, w1 = 0u, w2 = 0u;
+#pragma unroll
+      for (int bb = 0; bb < 4; ++bb) {
+        uint32_t b0, b1, b2;
+        x_digit3(bad ? 0.f : xv4[bb], e, b0, b1, b2);
+        w0 |= b0 << (8 * bb);
+        w1 |= b1 << (8 * bb);
+        w2 |= b2 << (8 * bb);
+      }
+      uint32_t* dst = s_xh + (size_t)item * kXWords;
+      dst[k] = w0;
+      dst[8 + k] = w1;
+      dst[16 + k] = w2;
+      if (k == 0) {
+        s_xs[item * kXSums] = 0.f;
+        s_xs[item * kXSums + 1] = bad ? __builtin_nanf("") : ldexpf(1.f, -e);
+      }
+    }
+  } else {
   for (int item = threadIdx.x; item < NN * ng; item += blockDim.x) {
     const int n = item / ng, gg = item % ng;
     if (n < a.n) {
@@ -223,6 +347,7 @@ gemv_kernel(GemvArgs a) {
       s_xs[item * kXSums] = 0.f;
       s_xs[item * kXSums + 1] = 1.f;
     }
+  }
   }
   __syncthreads();
 #pragma unroll
@@ -265,13 +390,34 @@ gemv_kernel(GemvArgs a) {
     float acc[NN][RS];
 #pragma unroll
     for (int j = 0; j < RS; ++j) {
+      float dA[NN], dB[NN];
+      if constexpr (kI8<FMT>) {
+      // block sums of code * digit: exact int32 dot products of the stored
+      // int8 codes (no decode), three digits per 4 columns
+      const uint32_t cw[8] = {cur[j].a.x, cur[j].a.y, cur[j].a.z, cur[j].a.w,
+                              cur[j].b.x, cur[j].b.y, cur[j].b.z, cur[j].b.w};
+#pragma unroll
+      for (int n = 0; n < NN; ++n) {
+        int a0 = 0, a1 = 0, a2 = 0, b0 = 0, b1 = 0, b2 = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          a0 = __builtin_amdgcn_sdot4((int)cw[k], (int)xh[n][k], a0, false);
+          a1 = __builtin_amdgcn_sdot4((int)cw[k], (int)xh[n][8 + k], a1, false);
+          a2 = __builtin_amdgcn_sdot4((int)cw[k], (int)xl[n][k], a2, false);
+          b0 = __builtin_amdgcn_sdot4((int)cw[4 + k], (int)xh[n][4 + k], b0, false);
+          b1 = __builtin_amdgcn_sdot4((int)cw[4 + k], (int)xh[n][12 + k], b1, false);
+          b2 = __builtin_amdgcn_sdot4((int)cw[4 + k], (int)xl[n][4 + k], b2, false);
+        }
+        dA[n] = digit_sum(a0, a1, a2) * xsc[n];
+        dB[n] = digit_sum(b0, b1, b2) * xsc[n];
+      }
+      } else {
       uint32_t h[16];
       decode_raw<FMT>(cur[j], h);
 #pragma unroll
       for (int i = 0; i < 16; ++i) h[i] = h2_bits(as_h2(h[i]) - bias2);
       // block sums of code * x (scaled by 2^e): the products are exact in
       // fp32, four independent chains
-      float dA[NN], dB[NN];
 #pragma unroll
       for (int n = 0; n < NN; ++n) {
         float ah = 0.f, al = 0.f, bh = 0.f, bl = 0.f;
@@ -287,6 +433,7 @@ gemv_kernel(GemvArgs a) {
         }
         dA[n] = (ah + al) * xsc[n];
         dB[n] = (bh + bl) * xsc[n];
+      }
       }
       if (FMT <= F_SB6_6) {
         const uint32_t rr[4] = {cur[j].b.x, cur[j].b.y, cur[j].b.z,

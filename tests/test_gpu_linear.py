@@ -130,6 +130,23 @@ def test_gemv_full_mantissa_and_range(kind, bits, n, scale):
     assert relmax(y, ref) < 1e-5
 
 
+@pytest.mark.parametrize("kind,bits", FORMATS)
+@pytest.mark.parametrize("n", [1, 2])
+def test_gemv_nonfinite_x_gives_nan(kind, bits, n):
+    """A NaN or inf in x makes the outputs it reaches NaN or inf, as in the
+    fp32 product, instead of a finite number (the int8 formats carry x as
+    integer digits, whose group scale then turns NaN)."""
+    lin = LIN[kind](qt_for(kind, bits, _w(256, 2048, seed=41)))
+    x = act(n, 2048, seed=42)
+    x[0, 100] = float("nan")
+    if n > 1:
+        x[1, 1000] = float("inf")
+    y = lin(x.cuda()).cpu().numpy()
+    assert not np.isfinite(y[0]).any()
+    if n > 1:
+        assert not np.isfinite(y[1]).any()
+
+
 @pytest.mark.parametrize("kind,bits", [("sb6", 5), ("sym", 6), ("rtn", 8)])
 def test_batched_rows_independent_of_batch(kind, bits):
     """A row's output is the same bits whatever else is in the batch and
