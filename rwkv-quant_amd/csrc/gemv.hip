@@ -19,9 +19,11 @@
 // two v_dot2_f32_f16 per code pair multiply the codes by hi and by lo with
 // exact products and fp32 sums, so the block sums carry x to about 22 bits
 // (fp32 x within the fp32 rounding of the sums).  The int8 formats (rtn8,
-// sym8) take x instead as three int8 digits under the group's power of two
-// (about 21 bits) and multiply the stored codes directly with exact int32
-// v_dot4_i32_i8 (no decode: head 29.6 -> 28.3 us).  Block scales follow the
+// sym8) and sb6@4 / @5 (unsigned codes) take x instead as three int8
+// digits under the group's power of two (about 21 bits) and multiply the
+// codes with exact int32 v_dot4_i32_i8: int8 codes as stored (rtn8 head
+// 29.6 -> 28.3 us), sb6 nibbles masked into bytes with the fifth bit
+// spread in (1.5B COMPRESSION decode 1.256 -> 1.185 ms).  Block scales follow the
 // format: s = f32(f16(qs * d)) (sb6 also m = f32(f16(qm * dm)), s clamped at
 // 1e-8), identical to the reference arithmetic
 // (reference: rwkv_quant/formats/codec.py:183-257,
@@ -78,11 +80,24 @@ struct GemvArgs {
 #ifndef RWKVQ_GEMV_I8DOT
 #define RWKVQ_GEMV_I8DOT 1
 #endif
-// int8 codes (rtn8, sym8) take x as three int8 digits instead of fp16
+#ifndef RWKVQ_GEMV_I8SB6
+#define RWKVQ_GEMV_I8SB6 1
+#endif
+// int8 codes (rtn8, sym8) and the 4- / 5-bit sb6 codes (unsigned, so they
+// fit an int8 as they are) take x as three int8 digits instead of fp16
 // hi + lo: the code products are then exact int32 dot products
-// (v_dot4_i32_i8, four columns per instruction, no decode of the codes).
+// (v_dot4_i32_i8, four columns per instruction).
 template <int FMT>
-constexpr bool kI8 = RWKVQ_GEMV_I8DOT && (FMT == F_RTN8 || FMT == F_SYM8);
+constexpr bool kI8 =
+    RWKVQ_GEMV_I8DOT &&
+    (FMT == F_RTN8 || FMT == F_SYM8 ||
+     (RWKVQ_GEMV_I8SB6 && (FMT == F_SB6_4 || FMT == F_SB6_5)));
+
+// Four bits b (bits 0..3) spread to bit 0 of bytes 0..3: the partial
+// products of the 24-bit multiply land 7 bits apart, so nothing carries.
+__device__ __forceinline__ uint32_t spread4(uint32_t b) {
+  return __umul24(b, 0x204081u) & 0x01010101u;
+}
 
 // Power of two for the int8 digits of a group whose largest |x| is amax:
 // amax 2^e in [63.75, 127.5), so the first digit fits [-127, 127].
@@ -111,16 +126,19 @@ __device__ __forceinline__ void x_digit3(float x, int e, uint32_t& b0,
 // One lane's 32 values of a group as digit words: w[0..7] first digits,
 // w[8..15] second, w[16..23] third (bytes in column order, word k = columns
 // 4k..4k+3); isc = 2^-e, NaN when the group holds a non-finite x (the
-// result is then NaN rather than a finite number).
+// result is then NaN rather than a finite number); sum = the fp32 sum of x
+// (the sb6 min term).
 __device__ __forceinline__ void x_digits(const float xv[32], uint32_t w[24],
-                                         float& isc) {
-  float amax = 0.f;
+                                         float& isc, float& sum) {
+  float amax = 0.f, sf = 0.f;
   bool bad = false;
 #pragma unroll
   for (int c = 0; c < 32; ++c) {
     amax = fmaxf(amax, fabsf(xv[c]));
     bad |= !(fabsf(xv[c]) <= 3.4e38f);
+    sf += xv[c];
   }
+  sum = sf;
   const int e = digit_exp(amax);
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
@@ -166,12 +184,11 @@ __device__ __forceinline__ void x_group_regs(const float* __restrict__ xp,
   }
   if constexpr (kI8<FMT>) {
     uint32_t w[24];
-    x_digits(xv, w, isc);
+    x_digits(xv, w, isc, sum);
 #pragma unroll
     for (int i = 0; i < 16; ++i) hi[i] = w[i];
 #pragma unroll
     for (int i = 0; i < 8; ++i) { lo[i] = w[16 + i]; lo[8 + i] = 0u; }
-    sum = 0.f;
     return;
   }
   float amax = 0.f, sf = 0.f;
@@ -309,10 +326,12 @@ gemv_kernel(GemvArgs a) {
                          fmaxf(fabsf(f.z), fabsf(f.w)));
       int bad = !(fabsf(f.x) <= 3.4e38f) | !(fabsf(f.y) <= 3.4e38f) |
                 !(fabsf(f.z) <= 3.4e38f) | !(fabsf(f.w) <= 3.4e38f);
+      float sf = (f.x + f.y) + (f.z + f.w);
 #pragma unroll
       for (int m = 1; m < 8; m <<= 1) {
         amax = fmaxf(amax, __shfl_xor(amax, m, 64));
         bad |= __shfl_xor(bad, m, 64);
+        sf += __shfl_xor(sf, m, 64);
       }
       const int e = digit_exp(amax);
       uint32_t w0 = 0u, w1 = 0u, w2 = 0u;
@@ -329,7 +348,7 @@ gemv_kernel(GemvArgs a) {
       dst[8 + k] = w1;
       dst[16 + k] = w2;
       if (k == 0) {
-        s_xs[item * kXSums] = 0.f;
+        s_xs[item * kXSums] = sf;
         s_xs[item * kXSums + 1] = bad ? __builtin_nanf("") : ldexpf(1.f, -e);
       }
     }
@@ -392,10 +411,29 @@ gemv_kernel(GemvArgs a) {
     for (int j = 0; j < RS; ++j) {
       float dA[NN], dB[NN];
       if constexpr (kI8<FMT>) {
-      // block sums of code * digit: exact int32 dot products of the stored
-      // int8 codes (no decode), three digits per 4 columns
-      const uint32_t cw[8] = {cur[j].a.x, cur[j].a.y, cur[j].a.z, cur[j].a.w,
-                              cur[j].b.x, cur[j].b.y, cur[j].b.z, cur[j].b.w};
+      // block sums of code * digit: exact int32 dot products, three digits
+      // per 4 columns.  int8 formats: the stored codes as they are; sb6:
+      // byte j of the nibble plane holds columns j (low nibble) and j + 16
+      // (high), so masking gives columns 0..15 and 16..31 in order, and the
+      // fifth bits (bit c of the group's word = column c) are spread in
+      uint32_t cw[8];
+      if constexpr (FMT == F_RTN8 || FMT == F_SYM8) {
+        cw[0] = cur[j].a.x; cw[1] = cur[j].a.y; cw[2] = cur[j].a.z;
+        cw[3] = cur[j].a.w; cw[4] = cur[j].b.x; cw[5] = cur[j].b.y;
+        cw[6] = cur[j].b.z; cw[7] = cur[j].b.w;
+      } else {
+        const uint32_t nw[4] = {cur[j].a.x, cur[j].a.y, cur[j].a.z, cur[j].a.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          cw[k] = nw[k] & 0x0F0F0F0Fu;
+          cw[4 + k] = (nw[k] >> 4) & 0x0F0F0F0Fu;
+          if constexpr (FMT == F_SB6_5) {
+            const uint32_t H = cur[j].h.x;
+            cw[k] |= spread4((H >> (4 * k)) & 15u) << 4;
+            cw[4 + k] |= spread4((H >> (16 + 4 * k)) & 15u) << 4;
+          }
+        }
+      }
 #pragma unroll
       for (int n = 0; n < NN; ++n) {
         int a0 = 0, a1 = 0, a2 = 0, b0 = 0, b1 = 0, b2 = 0;
