@@ -83,6 +83,9 @@ struct GemvArgs {
 #ifndef RWKVQ_GEMV_I8SB6
 #define RWKVQ_GEMV_I8SB6 1
 #endif
+#ifndef RWKVQ_GEMV_I8SYM6
+#define RWKVQ_GEMV_I8SYM6 1
+#endif
 // int8 codes (rtn8, sym8) and the 4- / 5-bit sb6 codes (unsigned, so they
 // fit an int8 as they are) take x as three int8 digits instead of fp16
 // hi + lo: the code products are then exact int32 dot products
@@ -91,7 +94,22 @@ template <int FMT>
 constexpr bool kI8 =
     RWKVQ_GEMV_I8DOT &&
     (FMT == F_RTN8 || FMT == F_SYM8 ||
-     (RWKVQ_GEMV_I8SB6 && (FMT == F_SB6_4 || FMT == F_SB6_5)));
+     (RWKVQ_GEMV_I8SB6 && (FMT == F_SB6_4 || FMT == F_SB6_5)) ||
+     (RWKVQ_GEMV_I8SYM6 && FMT == F_SYM6));
+
+// 4 x 4 byte transpose: out[t] byte b = in[b] byte t (eight v_perm_b32).
+__device__ __forceinline__ void byte_transpose4(uint32_t a, uint32_t b,
+                                                uint32_t c, uint32_t d,
+                                                uint32_t out[4]) {
+  const uint32_t t0 = __builtin_amdgcn_perm(b, a, 0x05010400u);  // a0 b0 a1 b1
+  const uint32_t t1 = __builtin_amdgcn_perm(b, a, 0x07030602u);  // a2 b2 a3 b3
+  const uint32_t t2 = __builtin_amdgcn_perm(d, c, 0x05010400u);  // c0 d0 c1 d1
+  const uint32_t t3 = __builtin_amdgcn_perm(d, c, 0x07030602u);  // c2 d2 c3 d3
+  out[0] = __builtin_amdgcn_perm(t2, t0, 0x05040100u);
+  out[1] = __builtin_amdgcn_perm(t2, t0, 0x07060302u);
+  out[2] = __builtin_amdgcn_perm(t3, t1, 0x05040100u);
+  out[3] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
+}
 
 // Four bits b (bits 0..3) spread to bit 0 of bytes 0..3: the partial
 // products of the 24-bit multiply land 7 bits apart, so nothing carries.
@@ -126,19 +144,21 @@ __device__ __forceinline__ void x_digit3(float x, int e, uint32_t& b0,
 // One lane's 32 values of a group as digit words: w[0..7] first digits,
 // w[8..15] second, w[16..23] third (bytes in column order, word k = columns
 // 4k..4k+3); isc = 2^-e, NaN when the group holds a non-finite x (the
-// result is then NaN rather than a finite number); sum = the fp32 sum of x
-// (the sb6 min term).
+// result is then NaN rather than a finite number); sum_a / sum_b = the fp32
+// sums of columns 0..15 / 16..31 (the sb6 min and sym6 storage-shift terms).
 __device__ __forceinline__ void x_digits(const float xv[32], uint32_t w[24],
-                                         float& isc, float& sum) {
-  float amax = 0.f, sf = 0.f;
+                                         float& isc, float& sum_a,
+                                         float& sum_b) {
+  float amax = 0.f, sa = 0.f, sb = 0.f;
   bool bad = false;
 #pragma unroll
   for (int c = 0; c < 32; ++c) {
     amax = fmaxf(amax, fabsf(xv[c]));
     bad |= !(fabsf(xv[c]) <= 3.4e38f);
-    sf += xv[c];
+    if (c < 16) sa += xv[c]; else sb += xv[c];
   }
-  sum = sf;
+  sum_a = sa;
+  sum_b = sb;
   const int e = digit_exp(amax);
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
@@ -169,12 +189,14 @@ __device__ __forceinline__ float digit_sum(int s0, int s1, int s2) {
 // the group's largest |x| in [2^14, 2^15): no fp16 overflow whatever the
 // range of x, and lo stays a normal fp16 down to 2^-17 of that maximum.
 // dst: 16 hi pairs, then 16 lo pairs; sums: the fp32 sum of x (the sb6
-// min term) and 2^-e.  int8 formats: the digit words of x_digits instead
-// (hi = first and second digits, lo[0..7] = third).
-template <int FMT>
+// min term), 2^-e and 0.  int8-digit formats: the digit words of x_digits
+// instead (hi = first and second digits, lo[0..7] = third) and the sums of
+// columns 0..15 and 16..31.
+template <int FMT, bool DIG = kI8<FMT>>
 __device__ __forceinline__ void x_group_regs(const float* __restrict__ xp,
                                              uint32_t hi[16], uint32_t lo[16],
-                                             float& sum, float& isc) {
+                                             float& sum, float& isc,
+                                             float& sum_b) {
   float xv[32];
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
@@ -182,9 +204,9 @@ __device__ __forceinline__ void x_group_regs(const float* __restrict__ xp,
     xv[4 * t] = f.x; xv[4 * t + 1] = f.y; xv[4 * t + 2] = f.z;
     xv[4 * t + 3] = f.w;
   }
-  if constexpr (kI8<FMT>) {
+  if constexpr (DIG) {
     uint32_t w[24];
-    x_digits(xv, w, isc, sum);
+    x_digits(xv, w, isc, sum, sum_b);
 #pragma unroll
     for (int i = 0; i < 16; ++i) hi[i] = w[i];
 #pragma unroll
@@ -210,6 +232,7 @@ __device__ __forceinline__ void x_group_regs(const float* __restrict__ xp,
     lo[i] = pack_h2(a0 - h2_lo(hi[i]), a1 - h2_hi(hi[i]));
   }
   sum = sf;
+  sum_b = 0.f;
   isc = ldexpf(1.f, -e);
 }
 
@@ -218,7 +241,7 @@ __device__ __forceinline__ void x_group(const float* __restrict__ xp,
                                         uint32_t* __restrict__ dst,
                                         float* __restrict__ sums) {
   uint32_t hi[16], lo[16];
-  x_group_regs<FMT>(xp, hi, lo, sums[0], sums[1]);
+  x_group_regs<FMT, false>(xp, hi, lo, sums[0], sums[1], sums[2]);
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     reinterpret_cast<uint4*>(dst)[q] =
@@ -229,7 +252,8 @@ __device__ __forceinline__ void x_group(const float* __restrict__ xp,
 }
 
 constexpr int kXWords = 32;   // staged words per (input row, group)
-constexpr int kXSums = 2;     // staged floats per (input row, group)
+constexpr int kXSums = 3;     // staged floats per (input row, group):
+                              // sum (cols 0..15 or all), 2^-e, sum 16..31
 
 // ILV: interleaved row order (the heads); otherwise blocked rows.  The
 // sb6 codes are read with non-temporal loads (1.5B COMPRESSION decode
@@ -291,8 +315,13 @@ gemv_kernel(GemvArgs a) {
                         nsb, gl, cur[j]);
 
   const int seg = !ILV && wg_row0 < a.rows ? wg_row0 / a.out_per : 0;
+  // the int8-digit products for one or two input rows (more rows would not
+  // fit the registers) with x staged in LDS: converted per lane (XD), the
+  // digits cost more than they save (8192-wide sym6 value GEMV 9.4 -> 10.7
+  // us; 1.5B sb6 decode 1.190 ms with hi + lo there, 1.202 ms with digits)
+  constexpr bool kDig = kI8<FMT> && NN <= 2 && !XD;
   uint32_t xh[NN][16], xl[NN][16];
-  float xsf[NN], xsc[NN];
+  float xsf[NN], xsc[NN], xsb[NN];
   if constexpr (XD) {
   // each lane converts its own group of x straight from global memory
   // (L2 after the first wave): no LDS round trip, no barrier before the
@@ -300,18 +329,20 @@ gemv_kernel(GemvArgs a) {
 #pragma unroll
   for (int n = 0; n < NN; ++n) {
     if (n < a.n) {
-      x_group_regs<FMT>(a.x + (size_t)n * a.x_ld + (size_t)seg * a.in +
+      x_group_regs<FMT, kDig>(a.x + (size_t)n * a.x_ld + (size_t)seg * a.in +
                             (size_t)gl * 32,
-                        xh[n], xl[n], xsf[n], xsc[n]);
+                        xh[n], xl[n], xsf[n], xsc[n], xsb[n]);
+      if constexpr (!kDig) xsb[n] = 0.f;
     } else {
 #pragma unroll
       for (int i = 0; i < 16; ++i) xh[n][i] = xl[n][i] = 0u;
       xsf[n] = 0.f;
       xsc[n] = 1.f;
+      xsb[n] = 0.f;
     }
   }
   } else {
-  if constexpr (kI8<FMT>) {
+  if constexpr (kDig) {
     // digits: 8 threads per (input row, group), 4 columns each; the
     // group's largest |x| through three butterflies over those 8 lanes
     for (int it = threadIdx.x; it < NN * ng * 8; it += blockDim.x) {
@@ -331,7 +362,7 @@ gemv_kernel(GemvArgs a) {
       for (int m = 1; m < 8; m <<= 1) {
         amax = fmaxf(amax, __shfl_xor(amax, m, 64));
         bad |= __shfl_xor(bad, m, 64);
-        sf += __shfl_xor(sf, m, 64);
+        if (m < 4) sf += __shfl_xor(sf, m, 64);   // sum of the half
       }
       const int e = digit_exp(amax);
       uint32_t w0 = 0u, w1 = 0u, w2 = 0u;
@@ -351,6 +382,7 @@ gemv_kernel(GemvArgs a) {
         s_xs[item * kXSums] = sf;
         s_xs[item * kXSums + 1] = bad ? __builtin_nanf("") : ldexpf(1.f, -e);
       }
+      if (k == 4) s_xs[item * kXSums + 2] = sf;
     }
   } else {
   for (int item = threadIdx.x; item < NN * ng; item += blockDim.x) {
@@ -365,6 +397,7 @@ gemv_kernel(GemvArgs a) {
       for (int q = 0; q < kXWords; ++q) s_xh[(size_t)item * kXWords + q] = 0u;
       s_xs[item * kXSums] = 0.f;
       s_xs[item * kXSums + 1] = 1.f;
+      s_xs[item * kXSums + 2] = 0.f;
     }
   }
   }
@@ -384,7 +417,24 @@ gemv_kernel(GemvArgs a) {
     }
     xsf[n] = s_xs[(n * ng + gl) * kXSums];
     xsc[n] = s_xs[(n * ng + gl) * kXSums + 1];
+    xsb[n] = kDig ? s_xs[(n * ng + gl) * kXSums + 2] : 0.f;
   }
+  }
+  // sym6: the digits once more in the order of the crumb words, whose
+  // (W >> 2t) & 0x03030303 holds the high bits of columns t, 4 + t, 8 + t,
+  // 12 + t of a 16-column half: xc[8 d + 4 h + t] (digit d, half h)
+  constexpr bool kCrumbDot = kDig && FMT == F_SYM6;
+  uint32_t xc[NN][kCrumbDot ? 24 : 1];
+  if constexpr (kCrumbDot) {
+#pragma unroll
+    for (int n = 0; n < NN; ++n)
+#pragma unroll
+      for (int d = 0; d < 3; ++d)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          const uint32_t* src = d < 2 ? &xh[n][8 * d + 4 * hh] : &xl[n][4 * hh];
+          byte_transpose4(src[0], src[1], src[2], src[3], &xc[n][8 * d + 4 * hh]);
+        }
   }
   // the decoder's fp16 pairs hold 1024 + code (+ the storage bias):
   // subtracting it in fp16 is exact and leaves the signed integer codes
@@ -410,14 +460,24 @@ gemv_kernel(GemvArgs a) {
 #pragma unroll
     for (int j = 0; j < RS; ++j) {
       float dA[NN], dB[NN];
-      if constexpr (kI8<FMT>) {
+      if constexpr (kDig) {
       // block sums of code * digit: exact int32 dot products, three digits
       // per 4 columns.  int8 formats: the stored codes as they are; sb6:
       // byte j of the nibble plane holds columns j (low nibble) and j + 16
       // (high), so masking gives columns 0..15 and 16..31 in order, and the
       // fifth bits (bit c of the group's word = column c) are spread in
       uint32_t cw[8];
-      if constexpr (FMT == F_RTN8 || FMT == F_SYM8) {
+      if constexpr (FMT == F_SYM6) {
+        // byte i of the nibble plane holds columns (i, i + 8) for i < 8 and
+        // (i + 8, i + 16) from 8 on: low nibbles of bytes 0..3 / 4..7 are
+        // columns 0..3 / 4..7, their high nibbles 8..11 / 12..15, and the
+        // same for bytes 8..15 and columns 16..31
+        const uint32_t nw[4] = {cur[j].a.x, cur[j].a.y, cur[j].a.z, cur[j].a.w};
+        cw[0] = nw[0] & 0x0F0F0F0Fu;         cw[1] = nw[1] & 0x0F0F0F0Fu;
+        cw[2] = (nw[0] >> 4) & 0x0F0F0F0Fu;  cw[3] = (nw[1] >> 4) & 0x0F0F0F0Fu;
+        cw[4] = nw[2] & 0x0F0F0F0Fu;         cw[5] = nw[3] & 0x0F0F0F0Fu;
+        cw[6] = (nw[2] >> 4) & 0x0F0F0F0Fu;  cw[7] = (nw[3] >> 4) & 0x0F0F0F0Fu;
+      } else if constexpr (FMT == F_RTN8 || FMT == F_SYM8) {
         cw[0] = cur[j].a.x; cw[1] = cur[j].a.y; cw[2] = cur[j].a.z;
         cw[3] = cur[j].a.w; cw[4] = cur[j].b.x; cw[5] = cur[j].b.y;
         cw[6] = cur[j].b.z; cw[7] = cur[j].b.w;
@@ -446,8 +506,29 @@ gemv_kernel(GemvArgs a) {
           b1 = __builtin_amdgcn_sdot4((int)cw[4 + k], (int)xh[n][12 + k], b1, false);
           b2 = __builtin_amdgcn_sdot4((int)cw[4 + k], (int)xl[n][4 + k], b2, false);
         }
+        if constexpr (kCrumbDot) {
+          // stored code u = nibble + 16 crumb = q + 32
+          const uint32_t W0 = cur[j].h.x, W1 = cur[j].h.y;
+          int ca0 = 0, ca1 = 0, ca2 = 0, cb0 = 0, cb1 = 0, cb2 = 0;
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const int c0 = (int)((W0 >> (2 * t)) & 0x03030303u);
+            const int c1 = (int)((W1 >> (2 * t)) & 0x03030303u);
+            ca0 = __builtin_amdgcn_sdot4(c0, (int)xc[n][t], ca0, false);
+            ca1 = __builtin_amdgcn_sdot4(c0, (int)xc[n][8 + t], ca1, false);
+            ca2 = __builtin_amdgcn_sdot4(c0, (int)xc[n][16 + t], ca2, false);
+            cb0 = __builtin_amdgcn_sdot4(c1, (int)xc[n][4 + t], cb0, false);
+            cb1 = __builtin_amdgcn_sdot4(c1, (int)xc[n][12 + t], cb1, false);
+            cb2 = __builtin_amdgcn_sdot4(c1, (int)xc[n][20 + t], cb2, false);
+          }
+          a0 += ca0 << 4; a1 += ca1 << 4; a2 += ca2 << 4;
+          b0 += cb0 << 4; b1 += cb1 << 4; b2 += cb2 << 4;
+          dA[n] = digit_sum(a0, a1, a2) * xsc[n] - 32.f * xsf[n];
+          dB[n] = digit_sum(b0, b1, b2) * xsc[n] - 32.f * xsb[n];
+        } else {
         dA[n] = digit_sum(a0, a1, a2) * xsc[n];
         dB[n] = digit_sum(b0, b1, b2) * xsc[n];
+        }
       }
       } else {
       uint32_t h[16];
@@ -488,7 +569,8 @@ gemv_kernel(GemvArgs a) {
         float m = f16_round((float)((int)qmv - 31) * dm);
 #pragma unroll
         for (int n = 0; n < NN; ++n)
-          acc[n][j] = active ? s * (dA[n] + dB[n]) + m * xsf[n] : 0.f;
+          acc[n][j] = active ? s * (dA[n] + dB[n]) + m * (xsf[n] + xsb[n])
+                             : 0.f;
       } else if (FMT == F_SYM6 || FMT == F_SYM8) {
         float d = f16_bits_to_f32(cur[j].dd);
         float sA = f16_round((float)(int8_t)(cur[j].s & 0xFFu) * d);
