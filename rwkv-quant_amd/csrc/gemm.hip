@@ -27,8 +27,9 @@
 // registers, nothing of W goes through LDS) and all BM tokens.  The K loop
 // takes 128 columns per step: lane half h decodes groups 2h and 2h+1 of
 // the step; x of the step (BM x 128, fp16, pair order) is staged in LDS,
-// double-buffered, one barrier per step.  Weights and x of step c + 1 are
-// loaded into registers before the MFMAs of step c.
+// double-buffered, one barrier per step.  x of step c + 1 is loaded into
+// registers at the start of step c, weights two steps ahead; each group's
+// decode is spread over the MFMA rounds before the ones that use it.
 //
 // Weight values (fp16, exactly as the format's dequant rounded once):
 //   sb6   w = fma(q, f16(s), f16(m))   (s = max(f32(f16(qs*d)), 1e-8))
@@ -41,9 +42,6 @@
 
 using namespace rwkvq;
 
-#ifndef RWKVQ_GEMM_BX_PIN
-#define RWKVQ_GEMM_BX_PIN 1
-#endif
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
@@ -166,19 +164,23 @@ __device__ __forceinline__ Raw group_of(const Raw2& w, int gi) {
   return r;
 }
 
-// fp16 weights of group gi of a Raw2 in the decoder's pair order (dense
-// fp16 rows: the stored values, natural order).
+// fp16 weights of group gi of a Raw2 in the decoder's pair order, a quad
+// (4 pairs) at a time: the group's scales, then pairs 4 qd .. 4 qd + 3
+// (dense fp16 rows: the stored values, natural order).
 template <int FMT>
-__device__ __forceinline__ void weights_of(const Raw2& r2, int gi, int kb,
-                                           uint32_t w[16]) {
+__device__ __forceinline__ DqScale scale_of(const Raw2& r2, int gi, int kb) {
+  if constexpr (FMT == F_F16) return DqScale{};
+  else return dq_scale<FMT>(group_of<FMT>(r2, gi), kb);
+}
+template <int FMT>
+__device__ __forceinline__ void quad_of(const Raw2& r2, int gi,
+                                        const DqScale& sc, int qd,
+                                        uint32_t w[16]) {
   if constexpr (FMT == F_F16) {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint4 v = r2.q[4 * gi + q];
-      w[4 * q] = v.x; w[4 * q + 1] = v.y; w[4 * q + 2] = v.z; w[4 * q + 3] = v.w;
-    }
+    const uint4 v = r2.q[4 * gi + qd];
+    w[4 * qd] = v.x; w[4 * qd + 1] = v.y; w[4 * qd + 2] = v.z; w[4 * qd + 3] = v.w;
   } else {
-    dequant_group<FMT>(group_of<FMT>(r2, gi), kb, w);
+    dq_quad<FMT>(group_of<FMT>(r2, gi), sc, qd, w);
   }
 }
 
@@ -323,20 +325,28 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a0, const int bid,
   __syncthreads();
 
   const int nsg = nrun / KG;                   // steps of each group
+  // Decode pipelined into the MFMA rounds: round k (k = 0..7) of a step
+  // multiplies with quad k % 4 of group k / 4 and decodes one quad of the
+  // next group due -- group 1 of the step in rounds 0-3, group 0 of the
+  // following step in rounds 4-7 -- so every MFMA has decode VALU work
+  // beside it instead of a block of decode in front of the rounds.
+  uint32_t w[2][WN][16];
+  {
+    const int c = c0 + kg;
+#pragma unroll
+    for (int ni = 0; ni < WN; ++ni) {
+      const DqScale sc = scale_of<FMT>(wset[0][ni], 0, (c * 4 + 2 * h) & 7);
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) quad_of<FMT>(wset[0][ni], 0, sc, qd, w[0][ni]);
+    }
+  }
   auto step = [&](int i, auto set_tag) __attribute__((always_inline)) {
     constexpr int S = decltype(set_tag)::value;   // register set of step i
     const int c = c0 + i * KG + kg;
-    // clamped to the group's last step: loads stay in W / x
     const int cn = min(c + KG, clast), cnn = min(c + 2 * KG, clast);
     load_x(cn);
-    // keep the loads of step c + KG ahead of this step's MFMAs: left to
-    // itself the scheduler sinks them next to their use
     __builtin_amdgcn_sched_barrier(0);
     const _Float16* xs = sx[kg][i & 1];
-    // The step's 8 MFMA rounds k = (group gi, 16-column sub-step ss) are
-    // software-pipelined: the x fragments of round k + 1 are read from LDS
-    // while round k's MFMAs run, and group 1's weights are decoded during
-    // group 0's rounds, so no MFMA waits on a just-issued LDS read.
     auto read_bx = [&](int k, half8_t (&b)[WM]) {
       const int gi = k >> 2, ss = k & 3;
 #pragma unroll
@@ -344,30 +354,25 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a0, const int bid,
         b[mi] = *reinterpret_cast<const half8_t*>(
             xs + (mi * 32 + r) * kRowH + (2 * h + gi) * 32 + ss * 8);
     };
-    uint32_t w[2][WN][16];
     half8_t bx[2][WM];
     read_bx(0, bx[0]);
+    DqScale sc[WN];
 #pragma unroll
     for (int ni = 0; ni < WN; ++ni)
-      weights_of<FMT>(wset[S][ni], 0, (c * 4 + 2 * h) & 7, w[0][ni]);
+      sc[ni] = scale_of<FMT>(wset[S][ni], 1, (c * 4 + 2 * h + 1) & 7);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       const int gi = k >> 2, ss = k & 3;
-      if (k + 1 < 8) read_bx(k + 1, bx[(k + 1) & 1]);
-#if RWKVQ_GEMM_BX_PIN
-      // the next round's x reads stay ahead of this round's MFMAs (left to
-      // itself the scheduler sinks them next to their use)
-      __builtin_amdgcn_sched_barrier(0);
-#endif
-      if (k == 1) {
-#pragma unroll
-        for (int ni = 0; ni < WN; ++ni)
-          weights_of<FMT>(wset[S][ni], 1, (c * 4 + 2 * h + 1) & 7, w[1][ni]);
-        // the set is decoded: refill it with step c + 2 KG
-        __builtin_amdgcn_sched_barrier(0);
+      if (k == 4) {
+        // group 1 of the step is decoded: refill its set with step c + 2 KG
         load_w(cnn, wset[S]);
         __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int ni = 0; ni < WN; ++ni)
+          sc[ni] = scale_of<FMT>(wset[1 - S][ni], 0, (cn * 4 + 2 * h) & 7);
       }
+      if (k + 1 < 8) read_bx(k + 1, bx[(k + 1) & 1]);
 #pragma unroll
       for (int ni = 0; ni < WN; ++ni) {
         const uint4 wa = make_uint4(w[gi][ni][4 * ss], w[gi][ni][4 * ss + 1],
@@ -379,9 +384,20 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a0, const int bid,
           acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
               av, bx[k & 1][mi], acc[mi][ni], 0, 0, 0);
       }
+#pragma unroll
+      for (int ni = 0; ni < WN; ++ni) {
+        if (k < 4) quad_of<FMT>(wset[S][ni], 1, sc[ni], k, w[1][ni]);
+        else quad_of<FMT>(wset[1 - S][ni], 0, sc[ni], k - 4, w[0][ni]);
+      }
+      // one MFMA, one x read, a share of the decode, ...
+#pragma unroll
+      for (int j = 0; j < WM * WN; ++j) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (k + 1 < 8 && j < WM) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 7, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
-    // the prefetched x registers are consumed only from here on
-    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int p = 0; p < XI; ++p) {
       if constexpr (XH) pin(xq[p]);
@@ -390,10 +406,16 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a0, const int bid,
     store_x((i + 1) & 1);
     __syncthreads();
   };
-  for (int i = 0; i < nsg; i += 2) {
+  // two steps per iteration and an odd last step after the loop (a path
+  // from the first step back to the loop head would carry that step's
+  // weight loads in flight and make every iteration wait for all loads at
+  // its head)
+  int i = 0;
+  for (; i + 1 < nsg; i += 2) {
     step(i, std::integral_constant<int, 0>());
-    if (i + 1 < nsg) step(i + 1, std::integral_constant<int, 1>());
+    step(i + 1, std::integral_constant<int, 1>());
   }
+  if (i < nsg) step(i, std::integral_constant<int, 0>());
 
   if constexpr (KG > 1) {
     // group 1 hands its sums to group 0 through the x buffers (free: the
@@ -706,8 +728,6 @@ GemmPlan plan_gemm(const GemmArgs& a, const SplitWs* ws) {
   };
   const int nsteps = a.in / kStepK;
   const bool wide = a.out_per % 256 == 0 && a.nseg_tab == 0;
-  // 256 x 128 tiles of 8 waves (32 rows x 128 tokens each; x staged once
-  // for 256 rows) where they alone give >= 256 workgroups
   if (wide && wgs(256, 128) >= 256) return {1, 4, 8, 1, true};
   if (RWKVQ_GEMM_SPLIT && a.M > 64) {
     // Two 4-wave workgroups per CU (each with its own barrier, so the two

@@ -184,6 +184,94 @@ __device__ __forceinline__ void dequant_group(const Raw& r, int kb,
   }
 }
 
+// dequant_group a quad (4 pairs) at a time, for kernels that spread one
+// group's decode over several matrix-core rounds: dq_scale once per group,
+// then dq_quad(qd) for qd = 0..3 gives pairs 4 qd .. 4 qd + 3, bit for bit
+// those of dequant_group.
+struct DqScale {
+  h2_t a, b;      // sb6: scale, min; sym: scales of pairs 0-7 and 8-15
+};
+
+template <int FMT>
+__device__ __forceinline__ DqScale dq_scale(const Raw& r, int kb) {
+  DqScale sc;
+  if (FMT <= F_SB6_6) {
+    const uint32_t rr[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
+    const int qs_word = (6 * kb) >> 5, qs_sh = (6 * kb) & 31;
+    const int qm_word = (48 + 6 * kb) >> 5, qm_sh = (48 + 6 * kb) & 31;
+    uint32_t lo = qs_word == 0 ? rr[0] : rr[1];
+    uint32_t hi = qs_word == 0 ? rr[1] : rr[2];
+    const uint32_t qsv = __builtin_amdgcn_alignbit(hi, lo, (uint32_t)qs_sh) & 63u;
+    lo = qm_word == 1 ? rr[1] : rr[2];
+    hi = qm_word == 1 ? rr[2] : rr[3];
+    const uint32_t qmv = __builtin_amdgcn_alignbit(hi, lo, (uint32_t)qm_sh) & 63u;
+    const float d = f16_bits_to_f32(rr[3] & 0xFFFFu);
+    const float dm = f16_bits_to_f32(rr[3] >> 16);
+    const _Float16 s = (_Float16)fmaxf(f16_round((float)qsv * d), 1e-8f);
+    const _Float16 m = (_Float16)((float)((int)qmv - 31) * dm);
+    sc.a = h2_t{s, s};
+    sc.b = h2_t{m, m};
+  } else if (FMT == F_SYM6 || FMT == F_SYM8) {
+    const float d = f16_bits_to_f32(r.dd);
+    const _Float16 sa = (_Float16)((float)(int8_t)(r.s & 0xFFu) * d);
+    const _Float16 sb = (_Float16)((float)(int8_t)((r.s >> 8) & 0xFFu) * d);
+    sc.a = h2_t{sa, sa};
+    sc.b = h2_t{sb, sb};
+  } else {
+    sc.a = h2_t{(_Float16)0.f, (_Float16)0.f};
+    sc.b = sc.a;
+  }
+  return sc;
+}
+
+template <int FMT>
+__device__ __forceinline__ void dq_quad(const Raw& r, const DqScale& sc,
+                                        int qd, uint32_t w[16]) {
+  uint32_t h[4];
+  if (FMT == F_SYM8 || FMT == F_RTN8) {
+    const uint32_t u0 = qd == 0 ? r.a.x : qd == 1 ? r.a.z : qd == 2 ? r.b.x : r.b.z;
+    const uint32_t u1 = qd == 0 ? r.a.y : qd == 1 ? r.a.w : qd == 2 ? r.b.y : r.b.w;
+    h[0] = i8_pair<0>(u0); h[1] = i8_pair<1>(u0);
+    h[2] = i8_pair<0>(u1); h[3] = i8_pair<1>(u1);
+  } else {
+    const uint32_t u = qd == 0 ? r.a.x : qd == 1 ? r.a.y : qd == 2 ? r.a.z : r.a.w;
+    const uint32_t us = u >> 4;
+    h[0] = nib_pair<0>(u, us); h[1] = nib_pair<1>(u, us);
+    h[2] = nib_pair<2>(u, us); h[3] = nib_pair<3>(u, us);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = 4 * qd + j;
+      if (FMT == F_SB6_5) {
+        const uint32_t hw = r.h.x;
+        h[j] |= __builtin_amdgcn_alignbit(hw, hw, (uint32_t)((i - 4) & 31)) &
+                0x00100010u;
+      } else if (FMT == F_SB6_6 || FMT == F_SYM6) {
+        const uint32_t H = (i < 8) ? r.h.x : r.h.y;
+        const int ip = i & 7;
+        h[j] |= __builtin_amdgcn_alignbit(H, H, (uint32_t)((2 * ip - 4) & 31)) &
+                0x00300030u;
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int i = 4 * qd + j;
+    if (FMT <= F_SB6_6) {
+      const h2_t bias = {(_Float16)1024.f, (_Float16)1024.f};
+      const h2_t q = as_h2(h[j]) - bias;                       // exact
+      w[i] = h2_bits(__builtin_elementwise_fma(q, sc.a, sc.b)); // one rounding
+    } else if (FMT == F_SYM6 || FMT == F_SYM8) {
+      const _Float16 mb = (_Float16)magic_bias<FMT>();
+      const h2_t bias = {mb, mb};
+      const h2_t q = as_h2(h[j]) - bias;                       // exact
+      w[i] = h2_bits(q * (i < 8 ? sc.a : sc.b));               // one rounding
+    } else {
+      const h2_t bias = {(_Float16)1152.f, (_Float16)1152.f};
+      w[i] = h2_bits(as_h2(h[j]) - bias);
+    }
+  }
+}
+
 // The format's fp32 weights of one (row, group) split into fp16 hi + lo
 // pairs (hi = f16(w), lo = f16(w - hi): w to about 22 bits), in the
 // decoder's pair order.  sb6 w = q s + m, sym w = q s (s, m the fp32
