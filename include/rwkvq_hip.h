@@ -513,6 +513,41 @@ int rwkvq_lora_down_q(int n_jobs, const uint8_t* const* q,
                       const int* rows, const int* epi, int in, int N,
                       void* stream);
 
+/* ------------------------------------------------- persistent decode
+ * Every layer of one batch-1 decode step in one launch of 256 workgroups
+ * (one per CU), five phases per layer separated by grid barriers: LN1 +
+ * token shift + lerp folded into the r/k/v GEMV rows and the LoRA down
+ * products (from the file's codes); the WKV step per head with the LoRA up
+ * products; the output projection (+= x); LN2 + shift + lerp folded into
+ * the key GEMV (relu^2); the value GEMV (+= x).  Each workgroup loads its
+ * next phase's weights while it waits at a barrier.
+ * layers: device array of L layer descriptors (the MkLayer struct of
+ * csrc/decode_mk.hip; its size from rwkvq_decode_mk_info); x [D] the
+ * residual stream after ln0, replaced by the last layer's output; act: the
+ * activation arena, act_floats >= L (6 D + F) floats (one region per layer
+ * and phase output, so each is written once per launch); x and act
+ * 128-byte aligned; vfirst [D]; the LoRA down outputs go to the regions
+ * the descriptors name (one 128-byte aligned region per layer); bar: bar_words uint32
+ * barrier words, zero before the first launch (every launch leaves them
+ * zero); err: set to 1 when a barrier wait ran past its spin limit (the
+ * results are then invalid).  Formats (fmt_proj, fmt_cmix): (1, 0) =
+ * sb6@5 projections / sb6@4 channel mix, (4, 3) = sym8 / sym6; D = 2048,
+ * F = 4 D, H = D / 64.  RWKVQ_ERR_SIZE when the device cannot hold all
+ * the workgroups at once.  Launches on one bar array must not overlap.
+ * Replaces: the per-layer decode body, one token per sequence (reference:
+ *   rwkv_quant/backends/metal/quant_model.py:638-728, 803-809). */
+int rwkvq_decode_mk(const void* layers, int L, int fmt_proj, int fmt_cmix,
+                    int D, int F, int H, float* x, float* act,
+                    long act_floats, float* vfirst, unsigned* bar, int* err,
+                    void* stream);
+
+/* Layout facts of rwkvq_decode_mk: the layer descriptor size in bytes,
+ * the barrier words, the workgroups per launch, the largest sum of LoRA
+ * ranks.  Any pointer may be null.
+ * Replaces: no reference function (the descriptor is this library's). */
+int rwkvq_decode_mk_info(int* layer_bytes, int* bar_words, int* wgs,
+                         int* max_cat);
+
 /* ------------------------------------------------------ perplexity
  * nll[r] = logsumexp(logits[r, :V]) - logits[r, target[r]] for r < rows
  * (one pass over each row, fixed reduction order); a target outside

@@ -88,6 +88,9 @@ SIGNATURES = {
     "rwkvq_wkv7_decode_lora_q": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                  _P, _P, _P, _P, _P, _I, _P, _P, _P, _I, _I,
                                  _I, _P],
+    "rwkvq_decode_mk": [_P, _I, _I, _I, _I, _I, _I, _P, _P, _L, _P, _P, _P,
+                        _P],
+    "rwkvq_decode_mk_info": [_P, _P, _P, _P],
 }
 
 _lib = None

@@ -34,6 +34,9 @@ Runtime switches (module attributes, as the reference's FUSE flags):
               step (one launch fewer per layer)
   USE_GRAPH   replay decode steps from a captured HIP graph
   LORA_FROM_CODES  decode LoRA from the file's codes (world checkpoints)
+  PERSISTENT_DECODE  batch-1 decode: every layer in one persistent launch
+              (rwkvq_decode_mk; five grid-barrier phases per layer) where
+              the model's shape and formats allow it
 """
 import ctypes
 from collections import OrderedDict
@@ -66,6 +69,7 @@ LORA_FROM_CODES = True         # decode LoRA (world checkpoints) read from
                                # (checked at run time, like FUSE_DECODE)
 LORA_Q_MAX_NC = 16384          # rows x width the code-based down kernel
                                # stages in LDS (64 KiB of fp32 x)
+PERSISTENT_DECODE = True       # batch-1 decode layers in one launch
 MAX_SEQ_GRAPHS = 8             # captured forward_stateful graphs kept (LRU);
                                # each owns its logits and two state sets
 
@@ -676,6 +680,7 @@ class QuantRWKV7:
         self._work = {}
         self._graphs = {}              # decode step graphs by batch size
         self._seq_graphs = OrderedDict()   # forward graphs by shape (LRU)
+        self._mk = None                # persistent decode (built on first use)
         torch.cuda.synchronize(dev)
 
     # ------------------------------------------------------------ state
@@ -689,6 +694,16 @@ class QuantRWKV7:
             self._work[N] = _Work(N, self.n_embd, self.ffn, self.ranks,
                                   self.device)
         return self._work[N]
+
+    def _persistent(self, B, T):
+        """The persistent decode kernel's host object when this step
+        (B sequences, T tokens) runs on it, else None."""
+        if not (PERSISTENT_DECODE and B == 1 and T == 1):
+            return None
+        if self._mk is None:
+            from .decode_mk import PersistentDecode
+            self._mk = PersistentDecode(self)
+        return self._mk if self._mk.ok else None
 
     # ---------------------------------------------------------- forward
     def _idx(self, idx):
@@ -712,6 +727,13 @@ class QuantRWKV7:
         self.emb.gather_into(idx.reshape(-1), x)
         _lib.call("rwkvq_layer_norm", _lib.ptr(x), _lib.ptr(self.ln0_w),
                   _lib.ptr(self.ln0_b), _lib.ptr(x), N, C, 1e-5, st)
+        mk = self._persistent(B, T)
+        if mk is not None:
+            mk.run(states, out_states, wk, st)
+            _lib.call("rwkvq_layer_norm", _lib.ptr(x),
+                      _lib.ptr(self.ln_out_w), _lib.ptr(self.ln_out_b),
+                      _lib.ptr(wk.xo), N, C, 1e-5, st)
+            return
         x16 = (X16_PREFILL and T > 1 and N >= GEMM_MIN_BATCH_NB
                and N > LORA_KERNEL_MAX_N)
         for li, (blk, state) in enumerate(zip(self.blocks, states)):
@@ -1006,6 +1028,10 @@ class QuantRWKV7:
             run(sets[0], sets[1])           # warm-up outside the graph
         torch.cuda.current_stream(dev).wait_stream(side)
         torch.cuda.synchronize(dev)
+        mk = self._persistent(B, 1)
+        if mk is not None:               # descriptor tables, both directions
+            mk.prepare(sets[0], sets[1], wk)
+            mk.prepare(sets[1], sets[0], wk)
         graphs = []
         for k in range(2):
             gph = torch.cuda.CUDAGraph()

@@ -1,0 +1,93 @@
+"""GPU parity of the persistent decode kernel (rwkvq_decode_mk): every layer
+of a batch-1 decode step in one launch, five grid-barrier phases per layer.
+
+Bars:
+* logits within 1e-2 max-abs of the float64 oracle (BASELINE.json
+  north_star), over several steps with the state carried;
+* against the per-kernel decode path of the same model (PERSISTENT_DECODE
+  off): logits within 5e-3 max-abs and states within 2e-3 -- the persistent
+  kernel stages every GEMV input as int8 digits (the per-kernel value GEMV
+  carries x as fp16 hi + lo) and sums the LoRA and row results in another
+  order, so a value can move by an fp32 rounding and carry into the later
+  layers; a wrong row, branch or phase order moves them by ~1e-1;
+* graph replay == eager launch, bit for bit (the kernel's reductions have a
+  fixed order; the barrier counters carry no data);
+* the barrier error flag stays clear (every wait ended within its limit).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle.rwkv7_ref import RWKV7Oracle
+from rwkv_quant.backends.hip import quant_model as qm
+from rwkv_quant.models.synthetic import quantized_model
+
+pytestmark = pytest.mark.gpu
+
+VOCAB = 1024
+
+
+@pytest.fixture(scope="module", params=["compression", "reduction"])
+def wide(request):
+    ck = quantized_model(request.param, n_layer=3, n_embd=2048, vocab=VOCAB,
+                         seed=41, device="cuda", to_cpu=True)
+    model = qm.QuantRWKV7(ck)
+    mk = model._persistent(1, 1)
+    assert mk is not None, model._mk.why
+    return ck, RWKV7Oracle(ck), model
+
+
+def _maxabs(a, b):
+    return float(np.abs(np.asarray(a, np.float64) - np.asarray(b)).max())
+
+
+def _eager(model, tok, st, persistent):
+    qm.PERSISTENT_DECODE = persistent
+    try:
+        lg, st2 = model.forward_stateful(torch.from_numpy(tok), st)
+    finally:
+        qm.PERSISTENT_DECODE = True
+    torch.cuda.synchronize()
+    return lg, st2
+
+
+def test_persistent_decode_matches_oracle_and_per_kernel_path(wide):
+    ck, orc, model = wide
+    print(f"persistent decode vs oracle / per-kernel", flush=True)
+    idx = np.random.default_rng(5).integers(0, VOCAB, size=(1, 6))
+    st_o = orc.init_state(1)
+    st_p, st_k = model.init_state(1), model.init_state(1)
+    for t in range(idx.shape[1]):
+        tok = idx[:, t:t + 1]
+        ro, st_o = orc.forward_stateful(tok, st_o)
+        lp, st_p = _eager(model, tok, st_p, True)
+        lk, st_k = _eager(model, tok, st_k, False)
+        assert not model._mk.error_flag()
+        assert np.isfinite(lp.cpu().numpy()).all()
+        assert _maxabs(lp.cpu().numpy(), ro) < 1e-2, t
+        assert _maxabs(lp.cpu().numpy(), lk.cpu().numpy()) < 5e-3, t
+        for (ap, bp, cp), (ak, bk, ck_) in zip(st_p, st_k):
+            for u, v in ((ap, ak), (bp, bk), (cp, ck_)):
+                assert _maxabs(u.cpu().numpy(), v.cpu().numpy()) < 2e-3, t
+
+
+def test_persistent_graph_replay_equals_eager(wide):
+    ck, orc, model = wide
+    print("persistent decode graph vs eager", flush=True)
+    idx = np.random.default_rng(6).integers(0, VOCAB, size=(1, 4))
+    st_g, st_e = model.init_state(1), model.init_state(1)
+    for t in range(idx.shape[1]):
+        tok = idx[:, t:t + 1]
+        lg, st_g = model.step(torch.from_numpy(tok), st_g)
+        le, st_e = _eager(model, tok, st_e, True)
+        assert torch.equal(lg, le), t
+        for a, b in zip(st_g, st_e):
+            for u, v in zip(a, b):
+                assert torch.equal(u, v), t
+    assert not model._mk.error_flag()
+
+
+def test_persistent_decode_disabled_for_batches(wide):
+    ck, orc, model = wide
+    assert model._persistent(2, 1) is None
+    assert model._persistent(1, 2) is None

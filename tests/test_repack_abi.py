@@ -90,3 +90,18 @@ def test_library_exports_every_declared_symbol():
         assert hasattr(lib, s), s
     # every declared symbol has a ctypes signature and vice versa
     assert set(syms) == set(_lib.SIGNATURES)
+
+
+def test_persistent_decode_descriptor_layout():
+    """The ctypes mirror of the persistent decode kernel's layer descriptor
+    has the size the library reports (a host-only call: no device)."""
+    from rwkv_quant.backends.hip.decode_mk import MkLayer
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.fail(f"{_lib.LIB_PATH} not built")
+    lb, bw, wgs, mc = (ctypes.c_int() for _ in range(4))
+    assert _lib.load().rwkvq_decode_mk_info(
+        ctypes.byref(lb), ctypes.byref(bw), ctypes.byref(wgs),
+        ctypes.byref(mc)) == 0
+    assert lb.value == ctypes.sizeof(MkLayer)
+    assert wgs.value == 256 and bw.value >= 2 * (wgs.value // 32) * 32 + 64
+    assert mc.value >= 288        # the 1.5B shape's four LoRA ranks
