@@ -62,57 +62,69 @@ constexpr int kMkCv = 10;          // 16-row LoRA-up code blocks per wave
 constexpr int kMkMaxCat = 4 * 16 * kMkCv;   // sum of the four ranks (640)
 constexpr int kBarWords = 2048;    // barrier workspace (uint32 words)
 
+// Descriptor pointers are typed global: read from the LDS copy of the
+// table, a pointer without an address space compiles to flat
+// instructions, which also count in the LDS counter (every LDS wait would
+// then also wait for the weight prefetch).
+// (host compilation parses the same structs with the default address
+// space; the layout is the same 64-bit pointers)
+#if defined(__HIP_DEVICE_COMPILE__)
+#define GLB __attribute__((address_space(1)))
+#else
+#define GLB
+#endif
+
 struct MkMat {                     // a packed matrix (load_raw's fields)
-  const uint8_t* q;
-  const uint32_t* hb;
-  const uint8_t* rec;
-  const int8_t* qs;
-  const uint16_t* d;
+  const GLB uint8_t* q;
+  const GLB uint32_t* hb;
+  const GLB uint8_t* rec;
+  const GLB int8_t* qs;
+  const GLB uint16_t* d;
   int rows, in;
 };
 
 struct MkDown {                    // one LoRA down product from the codes
-  const uint8_t* q;                // u8 asym / i8 codes [rows, D]
-  const float* s;                  // asym scale [rows / 64, D]; null: int8
-  const float* m;                  // asym min
-  const uint16_t* sc;              // int8: fp16 scale per input column [D]
-  float* y;                        // [rows]
+  const GLB uint8_t* q;                // u8 asym / i8 codes [rows, D]
+  const GLB float* s;                  // asym scale [rows / 64, D]; null: int8
+  const GLB float* m;                  // asym min
+  const GLB uint16_t* sc;              // int8: fp16 scale per input column [D]
+  GLB float* y;                        // [rows]
   int rows, slot, epi, wg0;        // lerp slot; first P1 workgroup (rel.)
 };
 
 struct MkUp {                      // LoRA up products (rwkvq_wkv7_decode_lora_q)
-  const float* h[4];               // the branches' down outputs (w a v g)
-  const uint8_t* q[4];
-  const float* s[4];
-  const float* m[4];
-  const uint16_t* sc[4];
+  const GLB float* h[4];               // the branches' down outputs (w a v g)
+  const GLB uint8_t* q[4];
+  const GLB float* s[4];
+  const GLB float* m[4];
+  const GLB uint16_t* sc[4];
   int r[4];
 };
 
 struct MkLayer {
   MkMat rkv, o, key, val;
-  const float* ln1_w;
-  const float* ln1_b;
-  const float* coef;               // [6, D] lerp coefficients r k v w a g
-  const float* tshift_in;          // [D] or null (zero shift)
-  float* tshift_out;
-  const float* ln2_w;
-  const float* ln2_b;
-  const float* xk;                 // [D]
-  const float* cshift_in;
-  float* cshift_out;
+  const GLB float* ln1_w;
+  const GLB float* ln1_b;
+  const GLB float* coef;               // [6, D] lerp coefficients r k v w a g
+  const GLB float* tshift_in;          // [D] or null (zero shift)
+  GLB float* tshift_out;
+  const GLB float* ln2_w;
+  const GLB float* ln2_b;
+  const GLB float* xk;                 // [D]
+  const GLB float* cshift_in;
+  GLB float* cshift_out;
   MkDown down[4];
   MkUp up;
-  const float* w0;
-  const float* a0;
-  const float* v0;
-  const float* k_k;
-  const float* k_a;
-  const float* r_k;
-  const float* lnx_w;
-  const float* lnx_b;
-  const float* state_in;           // [H, 64, 64]
-  float* state_out;
+  const GLB float* w0;
+  const GLB float* a0;
+  const GLB float* v0;
+  const GLB float* k_k;
+  const GLB float* k_a;
+  const GLB float* r_k;
+  const GLB float* lnx_w;
+  const GLB float* lnx_b;
+  const GLB float* state_in;           // [H, 64, 64]
+  GLB float* state_out;
   int n_down, layer0, lora_wgs, pad;
 };
 
@@ -628,7 +640,7 @@ decode_mk_k(MkArgs A) {
     for (int r = 0; r < 2; ++r)
 #pragma unroll
       for (int k = 0; k < KQ; ++k)
-        cq[r][k] = *reinterpret_cast<const uint32_t*>(
+        cq[r][k] = *reinterpret_cast<const GLB uint32_t*>(
             dn.q + (size_t)(rr + r) * D + 4 * (lane + 64 * k));
   };
   auto pf2 = [&](const MkLayer& Ly) {
@@ -643,7 +655,8 @@ decode_mk_k(MkArgs A) {
     // scales / mins of rank position tid
     if (tid < kHd) {
       const int c = h * kHd + tid;
-      pc0 = make_float4(Ly.w0[c], Ly.a0[c], Ly.k_k[c], Ly.k_a[c]);
+      pc0 = make_float4(Ly.w0[c], Ly.a0[c], Ly.k_k[c],
+                        Ly.k_a[c]);
       pc1 = make_float4(Ly.r_k[c], Ly.lnx_w[c], Ly.lnx_b[c],
                         Ly.layer0 ? 0.f : Ly.v0[c]);
     }
@@ -663,10 +676,10 @@ decode_mk_k(MkArgs A) {
     sm(u.s[2], u.m[2], u.sc[2], u.r[2], psv.z, pmv.z);
     sm(u.s[3], u.m[3], u.sc[3], u.r[3], psv.w, pmv.w);
     const int i = tid >> 2, part = tid & 3;
-    const float* sp = Ly.state_in + ((size_t)h * kHd + i) * kHd + part * 16;
+    const GLB float* sp = Ly.state_in + ((size_t)h * kHd + i) * kHd + part * 16;
 #pragma unroll
     for (int c = 0; c < 16; c += 4) {
-      const float4 q = *reinterpret_cast<const float4*>(sp + c);
+      const float4 q = *reinterpret_cast<const GLB float4*>(sp + c);
       S[c] = q.x; S[c + 1] = q.y; S[c + 2] = q.z; S[c + 3] = q.w;
     }
     const int o1 = u.r[0], o2 = o1 + u.r[1], o3 = o2 + u.r[2];
@@ -756,10 +769,10 @@ decode_mk_k(MkArgs A) {
         const int c0 = 4 * (lane + 64 * k);
         if (dn.s) {
           const size_t o = (size_t)(rr >> 6) * D + c0;
-          sv[k] = *reinterpret_cast<const uint4*>(dn.s + o);
-          mv[k] = *reinterpret_cast<const uint4*>(dn.m + o);
+          sv[k] = *reinterpret_cast<const GLB uint4*>(dn.s + o);
+          mv[k] = *reinterpret_cast<const GLB uint4*>(dn.m + o);
         } else {
-          scv[k] = *reinterpret_cast<const uint2*>(dn.sc + c0);
+          scv[k] = *reinterpret_cast<const GLB uint2*>(dn.sc + c0);
         }
       }
       LnIn<KE> li;
@@ -1004,7 +1017,8 @@ decode_mk_k(MkArgs A) {
     // ---------------- P4: LN2 + lerp, key rows, relu^2
     {
       LnIn<KE> li;
-      ln_load<KE>(li, a_xm, Ly.ln2_w, Ly.ln2_b, Ly.cshift_in, Ly.xk);
+      ln_load<KE>(li, a_xm, Ly.ln2_w, Ly.ln2_b, Ly.cshift_in,
+                  Ly.xk);
       ln_finish<KE>(li, s_row, wg == 0 ? Ly.cshift_out : nullptr, sh);
       lds_sync();
       {
