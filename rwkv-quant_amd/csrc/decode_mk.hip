@@ -129,8 +129,12 @@ struct MkLayer {
 };
 
 // Activations live in an arena with one region per (layer, phase output):
-// rkv [3 D], o [D], x after the output projection [D], key output [F], x
-// after the value GEMV [D] (the last layer's goes to x).  A region is
+// rkv [3 D], the WKV output [D], x after the output projection [D], the key
+// output [F], x after the value GEMV [D] (the last layer's goes to x).  The
+// WKV and key outputs are stored already as the consumer GEMV's int8
+// digits, 32 words per 32-column group (same size as the fp32 values), by
+// the workgroup that produces the group, so the consumers load them
+// instead of each converting the whole vector again.  A region is
 // written once per launch and read only after the barrier that follows
 // its writes, so no L2 of any XCD can hold an older copy of it (every L2 is
 // invalidated at kernel start): the readers use ordinary loads, and the
@@ -351,53 +355,118 @@ __device__ __forceinline__ void stage_load(StageIn<NG>& in, const float* src) {
     in.fv[i] = reinterpret_cast<const float4*>(src)[threadIdx.x + kT * i];
 }
 
+// One 32-column group as digits, computed by 8 consecutive lanes (aligned
+// to 8) holding 4 columns each (lane k: columns 4k .. 4k + 3): the group's
+// largest |x| and non-finite flag over all 8 lanes and the sums of each
+// half by DPP within the lane row (no LDS trip).  Returns the lane's three
+// digit words (columns 4k .. 4k + 3 of the first, second, third digit), the
+// half sum (lanes 0..3: columns 0..15, lanes 4..7: 16..31) and 2^-e (NaN
+// for a non-finite group).
+__device__ __forceinline__ void group_digits(float4 f, uint32_t& w0,
+                                             uint32_t& w1, uint32_t& w2,
+                                             float& sf, float& isc) {
+  const float xv4[4] = {f.x, f.y, f.z, f.w};
+  float amax = fmaxf(fmaxf(fabsf(f.x), fabsf(f.y)),
+                     fmaxf(fabsf(f.z), fabsf(f.w)));
+  float fb = (!(fabsf(f.x) <= 3.4e38f) | !(fabsf(f.y) <= 3.4e38f) |
+              !(fabsf(f.z) <= 3.4e38f) | !(fabsf(f.w) <= 3.4e38f))
+                 ? 1.f : 0.f;
+  sf = (f.x + f.y) + (f.z + f.w);
+  amax = fmaxf(amax, dpp_f<0xB1>(amax));      // quad_perm [1,0,3,2]
+  fb = fmaxf(fb, dpp_f<0xB1>(fb));
+  sf += dpp_f<0xB1>(sf);
+  amax = fmaxf(amax, dpp_f<0x4E>(amax));      // quad_perm [2,3,0,1]
+  fb = fmaxf(fb, dpp_f<0x4E>(fb));
+  sf += dpp_f<0x4E>(sf);
+  amax = fmaxf(amax, dpp_f<0x141>(amax));     // row_half_mirror: the
+  fb = fmaxf(fb, dpp_f<0x141>(fb));           // other quad of the 8
+  const bool bad = fb > 0.f;
+  const int e = digit_exp(amax);
+  w0 = w1 = w2 = 0u;
+#pragma unroll
+  for (int bb = 0; bb < 4; ++bb) {
+    uint32_t b0, b1, b2;
+    x_digit3(bad ? 0.f : xv4[bb], e, b0, b1, b2);
+    w0 |= b0 << (8 * bb);
+    w1 |= b1 << (8 * bb);
+    w2 |= b2 << (8 * bb);
+  }
+  isc = bad ? __builtin_nanf("") : ldexpf(1.f, -e);
+}
+
 template <int NG>
 __device__ __forceinline__ void stage_digits(const StageIn<NG>& in,
                                              uint32_t* s_xh, float* s_xs) {
   constexpr int NIT = StageIn<NG>::NIT;
-  const float4* fv = in.fv;
 #pragma unroll
   for (int i = 0; i < NIT; ++i) {
     const int it = threadIdx.x + kT * i;
     const int gg = it >> 3, k = it & 7;
-    const float4 f = fv[i];
-    const float xv4[4] = {f.x, f.y, f.z, f.w};
-    float amax = fmaxf(fmaxf(fabsf(f.x), fabsf(f.y)),
-                       fmaxf(fabsf(f.z), fabsf(f.w)));
-    int bad = !(fabsf(f.x) <= 3.4e38f) | !(fabsf(f.y) <= 3.4e38f) |
-              !(fabsf(f.z) <= 3.4e38f) | !(fabsf(f.w) <= 3.4e38f);
-    float sf = (f.x + f.y) + (f.z + f.w);
-    // the group's 8 lanes: largest |x| and non-finite flag over all 8, sums
-    // over each half (4 lanes), by DPP within the lane row (no LDS trip)
-    float fb = (float)bad;
-    amax = fmaxf(amax, dpp_f<0xB1>(amax));      // quad_perm [1,0,3,2]
-    fb = fmaxf(fb, dpp_f<0xB1>(fb));
-    sf += dpp_f<0xB1>(sf);
-    amax = fmaxf(amax, dpp_f<0x4E>(amax));      // quad_perm [2,3,0,1]
-    fb = fmaxf(fb, dpp_f<0x4E>(fb));
-    sf += dpp_f<0x4E>(sf);
-    amax = fmaxf(amax, dpp_f<0x141>(amax));     // row_half_mirror: the
-    fb = fmaxf(fb, dpp_f<0x141>(fb));           // other quad of the 8
-    bad = fb > 0.f;
-    const int e = digit_exp(amax);
-    uint32_t w0 = 0u, w1 = 0u, w2 = 0u;
-#pragma unroll
-    for (int bb = 0; bb < 4; ++bb) {
-      uint32_t b0, b1, b2;
-      x_digit3(bad ? 0.f : xv4[bb], e, b0, b1, b2);
-      w0 |= b0 << (8 * bb);
-      w1 |= b1 << (8 * bb);
-      w2 |= b2 << (8 * bb);
-    }
+    uint32_t w0, w1, w2;
+    float sf, isc;
+    group_digits(in.fv[i], w0, w1, w2, sf, isc);
     uint32_t* dst = s_xh + gg * 24;
     dst[k] = w0;
     dst[8 + k] = w1;
     dst[16 + k] = w2;
     if (k == 0) {
       s_xs[gg * 3] = sf;
-      s_xs[gg * 3 + 1] = bad ? __builtin_nanf("") : ldexpf(1.f, -e);
+      s_xs[gg * 3 + 1] = isc;
     }
     if (k == 4) s_xs[gg * 3 + 2] = sf;
+  }
+}
+
+// A producer's groups stored in global memory in the staged form: 32 words
+// per group (24 digit words, the sum of columns 0..15, 2^-e, the sum of
+// columns 16..31, 5 unused), written by the 8 lanes of the group.
+__device__ __forceinline__ void store_group_digits(float* g32, int k,
+                                                   uint32_t w0, uint32_t w1,
+                                                   uint32_t w2, float sf,
+                                                   float isc) {
+  act_st(g32 + k, __uint_as_float(w0));
+  act_st(g32 + 8 + k, __uint_as_float(w1));
+  act_st(g32 + 16 + k, __uint_as_float(w2));
+  if (k == 0) {
+    act_st(g32 + 24, sf);
+    act_st(g32 + 25, isc);
+  }
+  if (k == 4) act_st(g32 + 26, sf);
+}
+
+// Consumer: NG groups in that form (global) into the LDS staging layout.
+template <int NG>
+struct DigIn {
+  static constexpr int NIT = NG * 7 / kT + ((NG * 7) % kT != 0);
+  uint4 v[NIT];
+};
+
+template <int NG>
+__device__ __forceinline__ void dig_load(DigIn<NG>& in, const float* src) {
+#pragma unroll
+  for (int i = 0; i < DigIn<NG>::NIT; ++i) {
+    const int it = min((int)threadIdx.x + kT * i, NG * 7 - 1);
+    const int g = it / 7, q = it - 7 * (it / 7);
+    in.v[i] = reinterpret_cast<const uint4*>(src + g * 32)[q];
+  }
+}
+
+template <int NG>
+__device__ __forceinline__ void dig_store(const DigIn<NG>& in,
+                                          uint32_t* s_xh, float* s_xs) {
+#pragma unroll
+  for (int i = 0; i < DigIn<NG>::NIT; ++i) {
+    const int it = (int)threadIdx.x + kT * i;
+    if (it >= NG * 7) break;
+    const int g = it / 7, q = it - 7 * (it / 7);
+    const uint4 v = in.v[i];
+    if (q < 6) {
+      *reinterpret_cast<uint4*>(s_xh + g * 24 + 4 * q) = v;
+    } else {
+      s_xs[g * 3] = __uint_as_float(v.x);
+      s_xs[g * 3 + 1] = __uint_as_float(v.y);
+      s_xs[g * 3 + 2] = __uint_as_float(v.z);
+    }
   }
 }
 
@@ -573,6 +642,8 @@ decode_mk_k(MkArgs A) {
   constexpr bool NTP = FP <= F_SB6_6, NTC = FC <= F_SB6_6;
   static_assert(NGD == 64 && RPW3 >= 1 && RPG1 * kRkvWgs == 3 * D &&
                 D % RPG1 == 0, "decode kernel shape");
+  // a key workgroup's rows are one 32-column group of the value input
+  static_assert(4 * RPW4 == 32 && NGF == kG, "key rows per workgroup");
 
   extern __shared__ uint32_t smem[];
   // the layer descriptors, copied once: fields are then LDS reads instead
@@ -986,8 +1057,19 @@ decode_mk_k(MkArgs A) {
         const float dv = yy - mean;
         const float var = wave_sum_dpp(dv * dv) * (1.f / kHd);
         const float nrm = dv / sqrtf(var + 64e-5f);
-        act_st(a_o + h * kHd + tid,
-               ((nrm * lw + lb) + s_dp * vp) * s_up[3][tid]);
+        s_row[tid] = ((nrm * lw + lb) + s_dp * vp) * s_up[3][tid];
+      }
+      lds_sync();
+      // the head's 64 outputs = two groups of the output projection's
+      // input, stored once as digits (lanes 0..7 and 8..15 of wave 0)
+      if (wave == 0) {
+        const float4 f = reinterpret_cast<const float4*>(s_row)[lane & 15];
+        uint32_t w0, w1, w2;
+        float sf, isc;
+        group_digits(f, w0, w1, w2, sf, isc);
+        if (lane < 16)
+          store_group_digits(a_o + (2 * h + (lane >> 3)) * 32, lane & 7, w0,
+                             w1, w2, sf, isc);
       }
     }
     bar.arrive();
@@ -998,9 +1080,9 @@ decode_mk_k(MkArgs A) {
     {
       const int xr = gw * RPW3 + min(lane, RPW3 - 1);
       const float xres = a_xi[xr];         // in flight with the staging
-      StageIn<NGD> si;
-      stage_load<NGD>(si, a_o);
-      stage_digits<NGD>(si, s_xh, s_xs);
+      DigIn<NGD> di;
+      dig_load<NGD>(di, a_o);
+      dig_store<NGD>(di, s_xh, s_xs);
       lds_sync();
       XDig<FP> xd;
       xdig_load<FP>(xd, s_xh, s_xs, lane);
@@ -1034,7 +1116,18 @@ decode_mk_k(MkArgs A) {
       for (int j = 0; j < RPW4; ++j) acc[j] = group_dot<FC>(r4[j], xd, lane);
       float v = gather_rows<RPW4>(acc);
       v = v > 0.f ? v * v : 0.f;
-      if (lane < RPW4) act_st(a_hk + gw * RPW4 + lane, v);
+      // the workgroup's 32 rows are one group of the value product's input:
+      // stored once as digits (lanes 0..7 of wave 0)
+      if (lane < RPW4) s_row[wave * RPW4 + lane] = v;
+      lds_sync();
+      if (wave == 0) {
+        const float4 f = reinterpret_cast<const float4*>(s_row)[lane & 7];
+        uint32_t w0, w1, w2;
+        float sf, isc;
+        group_digits(f, w0, w1, w2, sf, isc);
+        if (lane < 8)
+          store_group_digits(a_hk + wg * 32, lane, w0, w1, w2, sf, isc);
+      }
     }
     bar.arrive();
     pf5(Ly);
@@ -1044,9 +1137,9 @@ decode_mk_k(MkArgs A) {
     {
       const int xr = gw * RPW3 + min(lane, RPW3 - 1);
       const float xres = a_xm[xr];
-      StageIn<NGF> si;
-      stage_load<NGF>(si, a_hk);
-      stage_digits<NGF>(si, s_xh, s_xs);
+      DigIn<NGF> di;
+      dig_load<NGF>(di, a_hk);
+      dig_store<NGF>(di, s_xh, s_xs);
       lds_sync();
       float acc[RPW3];
 #pragma unroll
