@@ -41,6 +41,7 @@
 // the format's block scales in fp32; the LoRA down products multiply the
 // dequantized fp32 weights (bit-exact with the dequant kernels) by fp32 x.
 #include <mutex>
+#include <type_traits>
 
 #include "qfmt.h"
 #include "rwkvq_hip.h"
@@ -963,35 +964,48 @@ decode_mk_k(MkArgs A) {
         s_bm[tid] = a;
       }
       lds_sync();
+      // Branch-free over the code blocks of the wave (blocks wave, wave + 4,
+      // ...), so the LDS reads of all blocks can be issued together: a block
+      // past the last one reads block 0 and adds nothing.  The branch of a
+      // block, its int8 flip and the accumulator it joins are selects.
+      const uint32_t amask = (u.s[0] ? 1u : 0u) | (u.s[1] ? 2u : 0u) |
+                             (u.s[2] ? 4u : 0u) | (u.s[3] ? 8u : 0u);
       float acc[4] = {0.f, 0.f, 0.f, 0.f};
+      auto up_blocks = [&](auto q0c, auto q1c) {
+        constexpr int Q0 = decltype(q0c)::value, Q1 = decltype(q1c)::value;
 #pragma unroll
-      for (int q = 0; q < kMkCv; ++q) {
-        const int b = wave + 4 * q;
-        if (b < nb) {
+        for (int q = Q0; q < Q1; ++q) {
+          const int b = wave + 4 * q;
+          const bool live = b < nb;
+          const int bc = live ? b : 0;
           const int p = 16 * b;
-          const int kb2 = p < o1 ? 0 : p < o2 ? 1 : p < o3 ? 2 : 3;
-          const bool asym = (kb2 == 0 ? u.s[0] : kb2 == 1 ? u.s[1]
-                             : kb2 == 2 ? u.s[2] : u.s[3]) != nullptr;
-          const uint32_t flip = asym ? 0u : 0x80808080u;
+          const int kb2 = (p >= o1) + (p >= o2) + (p >= o3);
+          const uint32_t flip = ((amask >> kb2) & 1u) ? 0u : 0x80808080u;
           const uint32_t wd[4] = {cv[q].x ^ flip, cv[q].y ^ flip,
                                   cv[q].z ^ flip, cv[q].w ^ flip};
           float d0 = 0.f, d1 = 0.f;
 #pragma unroll
           for (int qd = 0; qd < 4; ++qd) {
-            const float4 hs = s_hs4[4 * b + qd];
+            const float4 hs = s_hs4[4 * bc + qd];
             const uint32_t wv = wd[qd];
             d0 = fmaf((float)(wv & 0xFFu), hs.x, d0);
             d1 = fmaf((float)((wv >> 8) & 0xFFu), hs.y, d1);
             d0 = fmaf((float)((wv >> 16) & 0xFFu), hs.z, d0);
             d1 = fmaf((float)(wv >> 24), hs.w, d1);
           }
-          const float d = (d0 + d1) + s_bm[b];
-          if (kb2 == 0) acc[0] += d;
-          else if (kb2 == 1) acc[1] += d;
-          else if (kb2 == 2) acc[2] += d;
-          else acc[3] += d;
+          const float d = live ? (d0 + d1) + s_bm[bc] : 0.f;
+          acc[0] += kb2 == 0 ? d : 0.f;
+          acc[1] += kb2 == 1 ? d : 0.f;
+          acc[2] += kb2 == 2 ? d : 0.f;
+          acc[3] += kb2 == 3 ? d : 0.f;
         }
-      }
+      };
+      constexpr int kHalf = kMkCv / 2;
+      up_blocks(std::integral_constant<int, 0>{},
+                std::integral_constant<int, kHalf>{});
+      if (nb > 4 * kHalf)
+        up_blocks(std::integral_constant<int, kHalf>{},
+                  std::integral_constant<int, kMkCv>{});
 #pragma unroll
       for (int q = 0; q < 4; ++q) s_red[wave][q][lane] = acc[q];
       lds_sync();
