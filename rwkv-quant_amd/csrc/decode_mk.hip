@@ -672,6 +672,8 @@ decode_mk_k(MkArgs A) {
   // prefetched operands, one phase ahead
   Raw r1[RPW1];                        // P1 r/k/v rows
   uint32_t cq[2][KQ];                  // P1 LoRA down codes (2 rows / wave)
+  uint4 smv[KQ / 2];                   // P1 the workgroup's block scales /
+                                       // mins (asym) or column scales (int8)
   int jb = -1;                         // P1 LoRA job of this workgroup
   float S[16];                         // P2 state row slice
   uint4 cv[kMkCv];                     // P2 LoRA up code blocks
@@ -689,6 +691,8 @@ decode_mk_k(MkArgs A) {
     for (int r = 0; r < 2; ++r)
 #pragma unroll
       for (int k = 0; k < KQ; ++k) cq[r][k] = 0u;
+#pragma unroll
+    for (int q = 0; q < KQ / 2; ++q) smv[q] = make_uint4(0u, 0u, 0u, 0u);
     if (wg < kRkvWgs) {
       const int row0 = wg * RPG1 + wave * RPW1;
 #pragma unroll
@@ -714,6 +718,24 @@ decode_mk_k(MkArgs A) {
       for (int k = 0; k < KQ; ++k)
         cq[r][k] = *reinterpret_cast<const GLB uint32_t*>(
             dn.q + (size_t)(rr + r) * D + 4 * (lane + 64 * k));
+    // the block parameters of the workgroup's 8 rows (one 64-row block),
+    // once per workgroup: D scales and D mins (asym) or D fp16 column
+    // scales (int8), KQ / 2 16-byte words per thread
+    if (dn.s) {
+      const GLB uint4* sp = reinterpret_cast<const GLB uint4*>(
+          dn.s + (size_t)(rr >> 6) * D);
+      const GLB uint4* mp = reinterpret_cast<const GLB uint4*>(
+          dn.m + (size_t)(rr >> 6) * D);
+#pragma unroll
+      for (int q = 0; q < KQ / 4; ++q) {
+        smv[q] = sp[threadIdx.x + kT * q];
+        smv[KQ / 4 + q] = mp[threadIdx.x + kT * q];
+      }
+    } else {
+      const GLB uint4* cp = reinterpret_cast<const GLB uint4*>(dn.sc);
+#pragma unroll
+      for (int q = 0; q < KQ / 8; ++q) smv[q] = cp[threadIdx.x + kT * q];
+    }
   };
   auto pf2 = [&](const MkLayer& Ly) {
 #pragma unroll
@@ -830,23 +852,12 @@ decode_mk_k(MkArgs A) {
     } else if (jb >= 0) {
       const MkDown& dn = jb == 0 ? Ly.down[0] : jb == 1 ? Ly.down[1]
                        : jb == 2 ? Ly.down[2] : Ly.down[3];
-      // block parameters of the wave's rows: loaded with the row inputs
-      // below (one round trip), the codes were prefetched
-      const int rr = min((wg - kRkvWgs - dn.wg0) * 8 + wave * 2,
-                         dn.rows - 2);
-      uint4 sv[KQ], mv[KQ];
-      uint2 scv[KQ];
+      // the prefetched block parameters into LDS (the digit area is free in
+      // this role); visible after the LN's first barrier
+      float* s_sm = reinterpret_cast<float*>(s_xh);
 #pragma unroll
-      for (int k = 0; k < KQ; ++k) {
-        const int c0 = 4 * (lane + 64 * k);
-        if (dn.s) {
-          const size_t o = (size_t)(rr >> 6) * D + c0;
-          sv[k] = *reinterpret_cast<const GLB uint4*>(dn.s + o);
-          mv[k] = *reinterpret_cast<const GLB uint4*>(dn.m + o);
-        } else {
-          scv[k] = *reinterpret_cast<const GLB uint2*>(dn.sc + c0);
-        }
-      }
+      for (int q = 0; q < KQ / 2; ++q)
+        reinterpret_cast<uint4*>(s_sm)[threadIdx.x + kT * q] = smv[q];
       LnIn<KE> li;
       ln_load<KE>(li, a_xi, Ly.ln1_w, Ly.ln1_b, Ly.tshift_in,
                   Ly.coef + dn.slot * D);
@@ -857,15 +868,18 @@ decode_mk_k(MkArgs A) {
       float w[2][KQ][4];
 #pragma unroll
       for (int k = 0; k < KQ; ++k) {
+        const int c0 = 4 * (lane + 64 * k);
         float sk[4], mk[4] = {0.f, 0.f, 0.f, 0.f};
         if (dn.s) {
-          sk[0] = __uint_as_float(sv[k].x); sk[1] = __uint_as_float(sv[k].y);
-          sk[2] = __uint_as_float(sv[k].z); sk[3] = __uint_as_float(sv[k].w);
-          mk[0] = __uint_as_float(mv[k].x); mk[1] = __uint_as_float(mv[k].y);
-          mk[2] = __uint_as_float(mv[k].z); mk[3] = __uint_as_float(mv[k].w);
+          const float4 sv = *reinterpret_cast<const float4*>(s_sm + c0);
+          const float4 mv = *reinterpret_cast<const float4*>(s_sm + D + c0);
+          sk[0] = sv.x; sk[1] = sv.y; sk[2] = sv.z; sk[3] = sv.w;
+          mk[0] = mv.x; mk[1] = mv.y; mk[2] = mv.z; mk[3] = mv.w;
         } else {
-          sk[0] = h2_lo(scv[k].x); sk[1] = h2_hi(scv[k].x);
-          sk[2] = h2_lo(scv[k].y); sk[3] = h2_hi(scv[k].y);
+          const uint2 scv = *reinterpret_cast<const uint2*>(
+              reinterpret_cast<const uint16_t*>(s_sm) + c0);
+          sk[0] = h2_lo(scv.x); sk[1] = h2_hi(scv.x);
+          sk[2] = h2_lo(scv.y); sk[3] = h2_hi(scv.y);
         }
 #pragma unroll
         for (int r = 0; r < 2; ++r)
