@@ -272,6 +272,11 @@ def decode_bench(preset, batches, n_tok, dev, shape="1.5b", ceiling=None):
         out[f"b{B}_ms_per_step"] = round(ms, 4)
         out[f"b{B}_tok_s"] = round(B * 1e3 / ms, 1)
     add_decode_roofline(out, step_bytes, ceiling)
+    if 1 in batches:
+        # batch 1 runs every layer in one persistent launch where the shape
+        # and formats allow it (rwkvq_decode_mk), else one launch per kernel
+        out["b1_path"] = ("persistent" if model._persistent(1, 1) is not None
+                          else "per-kernel")
     return model, out
 
 
