@@ -541,6 +541,13 @@ int rwkvq_decode_mk(const void* layers, int L, int fmt_proj, int fmt_cmix,
                     long act_floats, float* vfirst, unsigned* bar, int* err,
                     void* stream);
 
+/* Failed polls of one barrier wait of rwkvq_decode_mk before it records the error
+ * flag and stops waiting (0 restores the default, 2^20).  A small limit
+ * forces the error path from the host: every wait then ends at once, the
+ * launch completes with invalid results and the flag set.
+ * Replaces: no reference function (a bound on this kernel's own waits). */
+int rwkvq_decode_mk_spin_limit(int limit);
+
 /* Layout facts of rwkvq_decode_mk: the layer descriptor size in bytes,
  * the barrier words, the workgroups per launch, the largest sum of LoRA
  * ranks.  Any pointer may be null.

@@ -58,7 +58,7 @@ constexpr int kW = kG * 4;         // waves per launch
 constexpr int kHd = 64;            // head size
 constexpr int kBarGroup = 32;      // workgroups per arrival counter
 constexpr int kNGrp = kG / kBarGroup;
-constexpr int kSpinLimit = 1 << 20;
+constexpr int kSpinLimit = 1 << 20;  // default polls per barrier wait
 constexpr int kRkvWgs = 192;       // P1 workgroups on the r/k/v rows
 constexpr int kMkCv = 10;          // 16-row LoRA-up code blocks per wave
 constexpr int kMkMaxCat = 4 * 16 * kMkCv;   // sum of the four ranks (640)
@@ -154,6 +154,7 @@ struct MkArgs {
   unsigned* bar;   // kBarWords words, zero between launches
   int* err;        // set to 1 when a barrier wait ran past its limit
   int L, H, act_stride;
+  int spin_limit;  // polls per barrier wait before the error is recorded
 };
 
 // ---- activations shared across workgroups (agent-scope, no L2 flush)
@@ -214,7 +215,7 @@ struct GridBar {
     }
   }
   // wave 0 polls every group's flag at once (lane g reads flag g)
-  __device__ void wait(int* err) {
+  __device__ void wait(int* err, int spin_limit) {
     if (threadIdx.x < 64) {
       const int lane = threadIdx.x;
       int spins = 0;
@@ -225,7 +226,7 @@ struct GridBar {
                               __HIP_MEMORY_SCOPE_AGENT) >= (unsigned)(k + 1);
         if (__all(ok)) break;
         __builtin_amdgcn_s_sleep(1);
-        if (++spins > kSpinLimit) {
+        if (++spins >= spin_limit) {
           if (lane == 0)
             __hip_atomic_store(err, 1, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
@@ -824,7 +825,7 @@ decode_mk_k(MkArgs A) {
     if (l > 0) {
       bar.arrive();
       pf1(Ly);
-      bar.wait(A.err);
+      bar.wait(A.err, A.spin_limit);
     }
     // ---------------- P1: LN1 + lerp, r/k/v rows, LoRA down products
     if (wg < kRkvWgs) {
@@ -910,7 +911,7 @@ decode_mk_k(MkArgs A) {
     }
     bar.arrive();
     pf2(Ly);
-    bar.wait(A.err);
+    bar.wait(A.err, A.spin_limit);
 
     // ---------------- P2: WKV step of head wg
     if (wg < A.H) {
@@ -1101,7 +1102,7 @@ decode_mk_k(MkArgs A) {
     }
     bar.arrive();
     pf3(Ly);
-    bar.wait(A.err);
+    bar.wait(A.err, A.spin_limit);
 
     // ---------------- P3: output projection, += residual
     {
@@ -1121,7 +1122,7 @@ decode_mk_k(MkArgs A) {
     }
     bar.arrive();
     pf4(Ly);
-    bar.wait(A.err);
+    bar.wait(A.err, A.spin_limit);
 
     // ---------------- P4: LN2 + lerp, key rows, relu^2
     {
@@ -1158,7 +1159,7 @@ decode_mk_k(MkArgs A) {
     }
     bar.arrive();
     pf5(Ly);
-    bar.wait(A.err);
+    bar.wait(A.err, A.spin_limit);
 
     // ---------------- P5: value rows (F wide), += residual
     {
@@ -1218,7 +1219,16 @@ bool mk_resident() {
 
 }  // namespace
 
+// Polls per barrier wait (host setting, read at each launch).
+int g_spin_limit = kSpinLimit;
+
 extern "C" {
+
+int rwkvq_decode_mk_spin_limit(int limit) {
+  if (limit < 0) return RWKVQ_ERR_ARG;
+  g_spin_limit = limit == 0 ? kSpinLimit : limit;
+  return RWKVQ_OK;
+}
 
 int rwkvq_decode_mk_info(int* layer_bytes, int* bar_words, int* wgs,
                          int* max_cat) {
@@ -1245,6 +1255,7 @@ int rwkvq_decode_mk(const void* layers, int L, int fmt_proj, int fmt_cmix,
   a.layers = static_cast<const MkLayer*>(layers);
   a.x = x; a.act = act; a.vfirst = vfirst;
   a.bar = bar; a.err = err; a.L = L; a.H = H; a.act_stride = (int)stride;
+  a.spin_limit = g_spin_limit;
   hipStream_t st = (hipStream_t)stream;
   static std::once_flag once;
   static bool ok_c = false, ok_r = false;

@@ -91,6 +91,7 @@ SIGNATURES = {
     "rwkvq_decode_mk": [_P, _I, _I, _I, _I, _I, _I, _P, _P, _L, _P, _P, _P,
                         _P],
     "rwkvq_decode_mk_info": [_P, _P, _P, _P],
+    "rwkvq_decode_mk_spin_limit": [_I],
 }
 
 _lib = None

@@ -223,5 +223,25 @@ class PersistentDecode:
                   _lib.ptr(self.bar), _lib.ptr(self.err), stream)
 
     def error_flag(self):
-        """True when some launch's barrier wait ran past its limit."""
+        """True when some launch's barrier wait ran past its limit (a
+        synchronizing read)."""
         return bool(self.err.item())
+
+    def check_deferred(self, stream):
+        """Raise if a launch checked by an earlier call set the error flag;
+        then queue an asynchronous copy of the flag for the next call.  No
+        synchronization: a launch is seen by the call after the copy has
+        landed (the flag is sticky, so a violation is never missed for
+        long).  A set flag means that not every workgroup was resident at
+        once -- the kernel must not share the device with concurrent work --
+        and that launch's results are invalid."""
+        if getattr(self, "_err_host", None) is None:
+            self._err_host = torch.zeros(1, dtype=torch.int32,
+                                         pin_memory=True)
+        elif int(self._err_host[0]):
+            raise _lib.HipKernelError(
+                "persistent decode: a grid-barrier wait ran past its limit "
+                "(not every workgroup was resident; concurrent kernels on "
+                "the device?) -- decode results are invalid")
+        with torch.cuda.stream(stream):
+            self._err_host.copy_(self.err, non_blocking=True)

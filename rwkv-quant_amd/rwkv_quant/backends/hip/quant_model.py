@@ -1001,6 +1001,9 @@ class QuantRWKV7:
         g["next"] = 0
         self._load_states(g["in"], states)
         g["graph"].replay()
+        mk = self._persistent(B, 1)
+        if mk is not None:
+            mk.check_deferred(torch.cuda.current_stream(self.device))
         new = [(s.clone(), t.clone(), c.clone()) for s, t, c in g["out"]]
         return g["logits"].clone().reshape(B, 1, -1), new
 

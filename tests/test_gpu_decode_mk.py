@@ -91,3 +91,35 @@ def test_persistent_decode_disabled_for_batches(wide):
     ck, orc, model = wide
     assert model._persistent(2, 1) is None
     assert model._persistent(1, 2) is None
+
+
+def test_barrier_timeout_is_reported(wide):
+    """A spin limit of one failed poll forces the barrier waits of an (eager)
+    launch to give up -- the launch still completes -- so the error flag is
+    set; a later step() raises (its check is deferred by one call, without
+    synchronizing).  The default limit is restored afterwards."""
+    from rwkv_quant.backends.hip import _lib
+    ck, orc, model = wide
+    mk = model._persistent(1, 1)
+    print("persistent decode forced barrier timeout", flush=True)
+    tok = torch.zeros(1, 1, dtype=torch.int64)
+    st = model.init_state(1)
+    try:
+        _lib.call("rwkvq_decode_mk_spin_limit", 1)
+        _, st = model.forward_stateful(tok, st)      # eager launch
+        torch.cuda.synchronize()
+        assert mk.error_flag()
+        _lib.call("rwkvq_decode_mk_spin_limit", 0)
+        with pytest.raises(_lib.HipKernelError):
+            for _ in range(2):
+                model.step(tok, st)
+                torch.cuda.synchronize()
+    finally:
+        _lib.call("rwkvq_decode_mk_spin_limit", 0)
+        torch.cuda.synchronize()
+        mk.err.zero_()
+        mk._err_host = None
+    for _ in range(2):
+        model.step(tok, model.init_state(1))
+        torch.cuda.synchronize()
+    assert not mk.error_flag()
