@@ -865,45 +865,55 @@ decode_mk_k(MkArgs A) {
       lds_sync();
       const int lw = wg - kRkvWgs;
       const int r0 = (lw - dn.wg0) * 8 + wave * 2;
-      float w[2][KQ][4];
-#pragma unroll
-      for (int k = 0; k < KQ; ++k) {
-        const int c0 = 4 * (lane + 64 * k);
-        float sk[4], mk[4] = {0.f, 0.f, 0.f, 0.f};
-        if (dn.s) {
-          const float4 sv = *reinterpret_cast<const float4*>(s_sm + c0);
-          const float4 mv = *reinterpret_cast<const float4*>(s_sm + D + c0);
-          sk[0] = sv.x; sk[1] = sv.y; sk[2] = sv.z; sk[3] = sv.w;
-          mk[0] = mv.x; mk[1] = mv.y; mk[2] = mv.z; mk[3] = mv.w;
-        } else {
-          const uint2 scv = *reinterpret_cast<const uint2*>(
-              reinterpret_cast<const uint16_t*>(s_sm) + c0);
-          sk[0] = h2_lo(scv.x); sk[1] = h2_hi(scv.x);
-          sk[2] = h2_lo(scv.y); sk[3] = h2_hi(scv.y);
-        }
-#pragma unroll
-        for (int r = 0; r < 2; ++r)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const uint32_t b = (cq[r][k] >> (8 * e)) & 0xFFu;
-            w[r][k][e] = dn.s ? dq_asym_1(b, sk[e], mk[e])
-                              : (float)(int)(int8_t)b * sk[e];
-          }
-      }
       const float4* xr = reinterpret_cast<const float4*>(s_row);
       float a0 = 0.f, a1 = 0.f;
+      // one body per code format, chosen by a wave-uniform (scalar) test:
+      // asym codes (fp32 scale and min per column) or int8 codes (fp16
+      // scale per column); each weight is the format's dequantized value
+      auto down_dot = [&](auto asym) {
+        // every LDS operand first (one wait), then the arithmetic
+        float4 sv[KQ], mv[KQ], xv[KQ];
 #pragma unroll
-      for (int k = 0; k < KQ; ++k) {
-        const float4 xv = xr[lane + 64 * k];
-        a0 = fmaf(xv.x, w[0][k][0], a0);
-        a1 = fmaf(xv.x, w[1][k][0], a1);
-        a0 = fmaf(xv.y, w[0][k][1], a0);
-        a1 = fmaf(xv.y, w[1][k][1], a1);
-        a0 = fmaf(xv.z, w[0][k][2], a0);
-        a1 = fmaf(xv.z, w[1][k][2], a1);
-        a0 = fmaf(xv.w, w[0][k][3], a0);
-        a1 = fmaf(xv.w, w[1][k][3], a1);
-      }
+        for (int k = 0; k < KQ; ++k) {
+          const int c0 = 4 * (lane + 64 * k);
+          if constexpr (decltype(asym)::value) {
+            sv[k] = *reinterpret_cast<const float4*>(s_sm + c0);
+            mv[k] = *reinterpret_cast<const float4*>(s_sm + D + c0);
+          } else {
+            const uint2 scv = *reinterpret_cast<const uint2*>(
+                reinterpret_cast<const uint16_t*>(s_sm) + c0);
+            sv[k] = make_float4(h2_lo(scv.x), h2_hi(scv.x), h2_lo(scv.y),
+                                h2_hi(scv.y));
+            mv[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+          }
+          xv[k] = xr[lane + 64 * k];
+        }
+#pragma unroll
+        for (int k = 0; k < KQ; ++k) {
+          const float sk[4] = {sv[k].x, sv[k].y, sv[k].z, sv[k].w};
+          const float mk[4] = {mv[k].x, mv[k].y, mv[k].z, mv[k].w};
+          const float xe[4] = {xv[k].x, xv[k].y, xv[k].z, xv[k].w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t b0 = (cq[0][k] >> (8 * e)) & 0xFFu;
+            const uint32_t b1 = (cq[1][k] >> (8 * e)) & 0xFFu;
+            float w0, w1;
+            if constexpr (decltype(asym)::value) {
+              w0 = dq_asym_1(b0, sk[e], mk[e]);
+              w1 = dq_asym_1(b1, sk[e], mk[e]);
+            } else {
+              w0 = (float)(int)(int8_t)b0 * sk[e];
+              w1 = (float)(int)(int8_t)b1 * sk[e];
+            }
+            a0 = fmaf(xe[e], w0, a0);
+            a1 = fmaf(xe[e], w1, a1);
+          }
+        }
+      };
+      if (__builtin_amdgcn_readfirstlane(dn.s != nullptr ? 1 : 0))
+        down_dot(std::integral_constant<bool, true>{});
+      else
+        down_dot(std::integral_constant<bool, false>{});
       a0 = wave_sum_dpp(a0);
       a1 = wave_sum_dpp(a1);
       if (r0 < dn.rows && lane < 2)
