@@ -259,10 +259,12 @@ struct GridBar {
 };
 
 // ---- block reductions (256 threads)
+// sh: 4 floats no wave reads or writes until every wave has passed the
+// barrier inside (each phase begins after the grid barrier's workgroup
+// barrier; the two sums of one LayerNorm use separate slots)
 __device__ __forceinline__ float block_sum(float v, float* sh) {
   v = wave_sum_dpp(v);
   const int w = threadIdx.x >> 6;
-  lds_sync();
   if ((threadIdx.x & 63) == 0) sh[w] = v;
   lds_sync();
   float s = 0.f;
@@ -300,9 +302,13 @@ __device__ __forceinline__ void ln_load(LnIn<KE>& in, const float* x,
   }
 }
 
+// s_out: the row into LDS (null: not stored); keep: the thread's KE float4s
+// of it in registers (null: not kept) -- columns 4 (t + 256 e), the lane
+// layout of the digit staging, so a GEMV phase stages from registers
 template <int KE>
 __device__ __forceinline__ void ln_finish(const LnIn<KE>& in, float* s_out,
-                                          float* shift_out, float* sh) {
+                                          float* shift_out, float* sh,
+                                          float4* keep = nullptr) {
   float s = 0.f;
 #pragma unroll
   for (int e = 0; e < KE; ++e)
@@ -316,7 +322,7 @@ __device__ __forceinline__ void ln_finish(const LnIn<KE>& in, float* s_out,
                 cc = in.v[e].z - mean, d = in.v[e].w - mean;
     q += (a * a + b * b) + (cc * cc + d * d);
   }
-  const float var = block_sum(q, sh) / (float)D;
+  const float var = block_sum(q, sh + 4) / (float)D;
   const float rstd = 1.f / sqrtf(var + 1e-5f);
 #pragma unroll
   for (int e = 0; e < KE; ++e) {
@@ -332,7 +338,8 @@ __device__ __forceinline__ void ln_finish(const LnIn<KE>& in, float* s_out,
     o.y = xn.y + (pv.y - xn.y) * cf.y;
     o.z = xn.z + (pv.z - xn.z) * cf.z;
     o.w = xn.w + (pv.w - xn.w) * cf.w;
-    *reinterpret_cast<float4*>(s_out + c) = o;
+    if (s_out) *reinterpret_cast<float4*>(s_out + c) = o;
+    if (keep) keep[e] = o;
     if (shift_out) *reinterpret_cast<float4*>(shift_out + c) = xn;
   }
 }
@@ -645,6 +652,8 @@ decode_mk_k(MkArgs A) {
                 D % RPG1 == 0, "decode kernel shape");
   // a key workgroup's rows are one 32-column group of the value input
   static_assert(4 * RPW4 == 32 && NGF == kG, "key rows per workgroup");
+  // the LayerNorm's registers are the digit staging's input
+  static_assert(StageIn<NGD>::NIT == KE, "LN / staging lane layout");
 
   extern __shared__ uint32_t smem[];
   // the layer descriptors, copied once: fields are then LDS reads instead
@@ -834,11 +843,10 @@ decode_mk_k(MkArgs A) {
       LnIn<KE> li;
       ln_load<KE>(li, a_xi, Ly.ln1_w, Ly.ln1_b, Ly.tshift_in,
                   Ly.coef + slot * D);
-      ln_finish<KE>(li, s_row, wg == 0 ? Ly.tshift_out : nullptr, sh);
-      lds_sync();
       {
         StageIn<NGD> si;
-        stage_load<NGD>(si, s_row);
+        ln_finish<KE>(li, nullptr, wg == 0 ? Ly.tshift_out : nullptr, sh,
+                      si.fv);
         stage_digits<NGD>(si, s_xh, s_xs);
       }
       lds_sync();
@@ -1139,11 +1147,10 @@ decode_mk_k(MkArgs A) {
       LnIn<KE> li;
       ln_load<KE>(li, a_xm, Ly.ln2_w, Ly.ln2_b, Ly.cshift_in,
                   Ly.xk);
-      ln_finish<KE>(li, s_row, wg == 0 ? Ly.cshift_out : nullptr, sh);
-      lds_sync();
       {
         StageIn<NGD> si;
-        stage_load<NGD>(si, s_row);
+        ln_finish<KE>(li, nullptr, wg == 0 ? Ly.cshift_out : nullptr, sh,
+                      si.fv);
         stage_digits<NGD>(si, s_xh, s_xs);
       }
       lds_sync();
