@@ -939,7 +939,6 @@ decode_mk_k(MkArgs A) {
       __shared__ float s_dp;
       __shared__ float s_up[4][kHd];
       __shared__ float4 s_hs4[kMkMaxCat / 4];
-      __shared__ float s_cj[kMkMaxCat];
       __shared__ float s_bm[kMkMaxCat / 16];
       __shared__ float s_red[4][4][kHd];
       float* s_hs = reinterpret_cast<float*>(s_hs4);
@@ -976,7 +975,6 @@ decode_mk_k(MkArgs A) {
 #pragma unroll
       for (int kb2 = 0; kb2 < 4; ++kb2) {
         const int rk = u.r[kb2];
-        if (tid >= rk) continue;
         const int off = kb2 == 0 ? 0 : kb2 == 1 ? o1 : kb2 == 2 ? o2 : o3;
         const bool asym = (kb2 == 0 ? u.s[0] : kb2 == 1 ? u.s[1]
                            : kb2 == 2 ? u.s[2] : u.s[3]) != nullptr;
@@ -985,15 +983,18 @@ decode_mk_k(MkArgs A) {
         const float mvk = kb2 == 0 ? pmv.x : kb2 == 1 ? pmv.y
                         : kb2 == 2 ? pmv.z : pmv.w;
         const float hs = hv[kb2] * svk;
-        s_hs[off + tid] = hs;
-        s_cj[off + tid] = asym ? hv[kb2] * mvk : -128.f * hs;
-      }
-      lds_sync();
-      if (tid < nb) {
-        float a = 0.f;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) a += s_cj[16 * tid + e];
-        s_bm[tid] = a;
+        // the block term of each 16-rank code block: ranks are multiples
+        // of 16, so a block's positions are the 16 lanes of one DPP row
+        // (all active or all past the rank)
+        float bm = asym ? hv[kb2] * mvk : -128.f * hs;
+        bm += dpp_f<0xB1>(bm);
+        bm += dpp_f<0x4E>(bm);
+        bm += dpp_f<0x141>(bm);
+        bm += dpp_f<0x140>(bm);
+        if (tid < rk) {
+          s_hs[off + tid] = hs;
+          if ((tid & 15) == 0) s_bm[(off + tid) >> 4] = bm;
+        }
       }
       lds_sync();
       // Branch-free over the code blocks of the wave (blocks wave, wave + 4,
@@ -1105,10 +1106,11 @@ decode_mk_k(MkArgs A) {
         const float nrm = dv / sqrtf(var + 64e-5f);
         s_row[tid] = ((nrm * lw + lb) + s_dp * vp) * s_up[3][tid];
       }
-      lds_sync();
       // the head's 64 outputs = two groups of the output projection's
-      // input, stored once as digits (lanes 0..7 and 8..15 of wave 0)
+      // input, stored once as digits (lanes 0..7 and 8..15 of wave 0);
+      // wave 0 wrote all 64 and reads its own LDS writes (in order)
       if (wave == 0) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         const float4 f = reinterpret_cast<const float4*>(s_row)[lane & 15];
         uint32_t w0, w1, w2;
         float sf, isc;
