@@ -1006,11 +1006,25 @@ decode_mk_k(MkArgs A) {
       float acc[4] = {0.f, 0.f, 0.f, 0.f};
       auto up_blocks = [&](auto q0c, auto q1c) {
         constexpr int Q0 = decltype(q0c)::value, Q1 = decltype(q1c)::value;
+        constexpr int NQ = Q1 - Q0;
+        // every LDS read of the chunk in flight before the first use
+        float4 hsv[NQ][4];
+        float bmv[NQ];
 #pragma unroll
         for (int q = Q0; q < Q1; ++q) {
           const int b = wave + 4 * q;
-          const bool live = b < nb;
-          const int bc = live ? b : 0;
+          const int bc = b < nb ? b : 0;
+#pragma unroll
+          for (int qd = 0; qd < 4; ++qd) hsv[q - Q0][qd] = s_hs4[4 * bc + qd];
+          bmv[q - Q0] = s_bm[bc];
+        }
+#pragma unroll
+        for (int q = Q0; q < Q1; ++q) {
+          const int b = wave + 4 * q;
+          // 1 for a live block, 0 past the last one; opaque to the
+          // compiler, which would otherwise branch around each block
+          float lm = b < nb ? 1.f : 0.f;
+          asm volatile("" : "+v"(lm));
           const int p = 16 * b;
           const int kb2 = (p >= o1) + (p >= o2) + (p >= o3);
           const uint32_t flip = ((amask >> kb2) & 1u) ? 0u : 0x80808080u;
@@ -1019,14 +1033,14 @@ decode_mk_k(MkArgs A) {
           float d0 = 0.f, d1 = 0.f;
 #pragma unroll
           for (int qd = 0; qd < 4; ++qd) {
-            const float4 hs = s_hs4[4 * bc + qd];
+            const float4 hs = hsv[q - Q0][qd];
             const uint32_t wv = wd[qd];
             d0 = fmaf((float)(wv & 0xFFu), hs.x, d0);
             d1 = fmaf((float)((wv >> 8) & 0xFFu), hs.y, d1);
             d0 = fmaf((float)((wv >> 16) & 0xFFu), hs.z, d0);
             d1 = fmaf((float)(wv >> 24), hs.w, d1);
           }
-          const float d = live ? (d0 + d1) + s_bm[bc] : 0.f;
+          const float d = ((d0 + d1) + bmv[q - Q0]) * lm;
           acc[0] += kb2 == 0 ? d : 0.f;
           acc[1] += kb2 == 1 ? d : 0.f;
           acc[2] += kb2 == 2 ? d : 0.f;
