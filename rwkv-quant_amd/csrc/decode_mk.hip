@@ -1047,12 +1047,17 @@ decode_mk_k(MkArgs A) {
           acc[3] += kb2 == 3 ? d : 0.f;
         }
       };
-      constexpr int kHalf = kMkCv / 2;
+      // chunks of 4, 4 and 2 blocks per wave: 32 blocks (ranks 512) run
+      // exactly two chunks, no dead slot
+      static_assert(kMkCv == 10, "up-product chunks");
       up_blocks(std::integral_constant<int, 0>{},
-                std::integral_constant<int, kHalf>{});
-      if (nb > 4 * kHalf)
-        up_blocks(std::integral_constant<int, kHalf>{},
-                  std::integral_constant<int, kMkCv>{});
+                std::integral_constant<int, 4>{});
+      if (nb > 16)
+        up_blocks(std::integral_constant<int, 4>{},
+                  std::integral_constant<int, 8>{});
+      if (nb > 32)
+        up_blocks(std::integral_constant<int, 8>{},
+                  std::integral_constant<int, 10>{});
 #pragma unroll
       for (int q = 0; q < 4; ++q) s_red[wave][q][lane] = acc[q];
       lds_sync();
