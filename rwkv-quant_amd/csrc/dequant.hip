@@ -69,6 +69,57 @@ __global__ void dq_sb6(const uint8_t* nib, const uint32_t* hb,
   }
 }
 
+// Row gather of sb6 codes (the embedding lookup, a few rows): one thread
+// per 8 consecutive columns of a 32-column group -- the group's 16-byte
+// record and the thread's 8 code bytes in one load each, the 8 outputs in
+// two float4 stores (consecutive threads, consecutive columns).  Per
+// column the arithmetic of dq_sb6.
+__global__ void gather_sb6(const uint8_t* nib, const uint32_t* hb,
+                           const uint8_t* rec, int bits, int n, int in,
+                           float* w, const int64_t* idx, int src_rows) {
+  const int per_row = in >> 3;
+  const long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (long)n * per_row) return;
+  const int orow = (int)(t / per_row), k = (int)(t % per_row);
+  const int g = k >> 2, qq = k & 3;
+  const int ng = in >> 5, nsb = in >> 8;
+  const int row = src_row(idx, orow, src_rows);
+  // record bytes 0..5: the 6-bit qs fields, 6..11: the qm fields,
+  // 12..13: d, 14..15: dm (fp16)
+  const uint4 r4 = *reinterpret_cast<const uint4*>(
+      rec + ((size_t)row * nsb + (g >> 3)) * 16);
+  const uint64_t s0 = (uint64_t)r4.x | ((uint64_t)(r4.y & 0xFFFFu) << 32);
+  const uint64_t s1 = (uint64_t)(r4.y >> 16) | ((uint64_t)r4.z << 16);
+  const int kb = g & 7;
+  const uint32_t qs = (uint32_t)(s0 >> (6 * kb)) & 63u;
+  const int qm = (int)((uint32_t)(s1 >> (6 * kb)) & 63u) - 31;
+  const float d = f16_bits_to_f32(r4.w & 0xFFFFu);
+  const float dm = f16_bits_to_f32(r4.w >> 16);
+  const float s = fmaxf(f16_round(((float)qs * d)), 1e-8f);
+  const float m = f16_round(((float)qm * dm));
+  // columns 8 qq .. 8 qq + 7: code bytes i0 .. i0 + 7, low or high nibbles
+  const int i0 = (qq & 1) * 8, half = qq >> 1;
+  const size_t gi = (size_t)row * ng + g;
+  const uint2 nb = *reinterpret_cast<const uint2*>(nib + gi * 16 + i0);
+  const uint32_t hw5 = bits == 5 ? hb[gi] : 0u;
+  float o[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int i = i0 + j, c = half * 16 + i;
+    const uint32_t byte = ((j < 4 ? nb.x : nb.y) >> (8 * (j & 3))) & 0xFFu;
+    uint32_t q = half ? (byte >> 4) : (byte & 15u);
+    if (bits == 5) {
+      q |= ((hw5 >> c) & 1u) << 4;
+    } else if (bits == 6) {
+      q |= high_bits_crumb(hb + gi * 2, i, half) << 4;
+    }
+    o[j] = (float)q * s + m;
+  }
+  float4* out = reinterpret_cast<float4*>(w + (size_t)orow * in + 8 * k);
+  out[0] = make_float4(o[0], o[1], o[2], o[3]);
+  out[1] = make_float4(o[4], o[5], o[6], o[7]);
+}
+
 __global__ void dq_sym(const uint8_t* codes, const uint32_t* hb,
                        const int8_t* qsp, const uint16_t* dp, int bits,
                        int rows, int in, float* w, int ld, const int64_t* idx,
@@ -318,9 +369,10 @@ int rwkvq_gather_rows_f32(int kind, int bits, const uint8_t* q,
   if (kind == 0) {            // sb6: aux0 = rec
     if (in % 256 || bits < 4 || bits > 6 || (bits > 4 && !hb))
       return RWKVQ_ERR_ARG;
-    long n = (long)n_idx * (in / 32);
-    hipLaunchKernelGGL(dq_sb6, grid_for(n, 256), dim3(256), 0, s, q, hb,
-                       (const uint8_t*)aux0, bits, n_idx, in, out, in, idx,
+    if (reinterpret_cast<uintptr_t>(out) & 15) return RWKVQ_ERR_ARG;
+    long n = (long)n_idx * (in / 8);
+    hipLaunchKernelGGL(gather_sb6, grid_for(n, 256), dim3(256), 0, s, q, hb,
+                       (const uint8_t*)aux0, bits, n_idx, in, out, idx,
                        src_rows);
   } else if (kind == 1) {     // sym: aux0 = qs, aux1 = d
     if (in % 256 || (bits != 6 && bits != 8) || (bits == 6 && !hb))

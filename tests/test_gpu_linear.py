@@ -200,3 +200,26 @@ def test_shape_errors_raise():
         _lib.call("rwkvq_gemv_sb6", _lib.ptr(lin.nib), None,
                   _lib.ptr(lin.rec), 4, 64, 500, 64, None, 0, None, 1, 0,
                   _lib.stream_handle())
+
+
+@pytest.mark.parametrize("bits", [4, 5, 6])
+@pytest.mark.parametrize("n_idx", [1, 8, 37])
+def test_gather_rows_sb6_bit_exact(bits, n_idx):
+    """The embedding gather (rwkvq_gather_rows_f32, sb6) == rows of the
+    oracle dequant bit for bit, indices clamped into the table."""
+    print(f"gather sb6@{bits} n_idx {n_idx}", flush=True)
+    w = _w(40, 2560, seed=17, degenerate=True, outliers=3)
+    qt = qt_for("sb6", bits, w)
+    lin = GwQuantLinear(qt)
+    rng = np.random.default_rng(n_idx)
+    ids = rng.integers(0, 40, size=n_idx)
+    ids[0] = 39
+    if n_idx > 2:
+        ids[1], ids[2] = -5, 1000          # clamped to 0 and 39
+    idx = torch.from_numpy(ids.astype(np.int64)).cuda()
+    out = torch.full((n_idx, 2560), float("nan"), device="cuda")
+    _lib.call("rwkvq_gather_rows_f32", 0, bits, _lib.ptr(lin.nib),
+              _lib.ptr(lin.hb), _lib.ptr(lin.rec), None, 40, 2560,
+              _lib.ptr(idx), n_idx, _lib.ptr(out), _lib.stream_handle())
+    ref = cr.dequant_qt(qt)[np.clip(ids, 0, 39)]
+    _assert_same_bits(out.cpu().numpy(), ref)
