@@ -239,8 +239,8 @@ int rwkvq_dequant_f16(int fmt, const uint8_t* q, const uint32_t* hb,
  * out[o, :] = dequant(W)[min(max(idx[o], 0), src_rows - 1), :], o < n_idx.
  * kind 0 = sb6 (q = nib, hb, aux0 = rec), 1 = sym (q = codes, hb,
  * aux0 = qs, aux1 = d), 2 = rtn@8 (q = codes, aux1 = scale).  Values are
- * bit-exact with the dequant entry points above.  kind 0 needs `out`
- * 16-byte aligned (RWKVQ_ERR_ARG otherwise).
+ * bit-exact with the dequant entry points above.  Kinds 0 and 1 need
+ * `out` 16-byte aligned (RWKVQ_ERR_ARG otherwise).
  * Replaces: the emb gather on the dense table
  *   (reference: rwkv_quant/backends/metal/quant_model.py:853, 975). */
 int rwkvq_gather_rows_f32(int kind, int bits, const uint8_t* q,

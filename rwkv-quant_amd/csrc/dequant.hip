@@ -150,6 +150,52 @@ __global__ void dq_sym(const uint8_t* codes, const uint32_t* hb,
   }
 }
 
+// Row gather of sym codes, laid out as gather_sb6 (8 consecutive columns
+// per thread, two float4 stores); per column the arithmetic of dq_sym.
+// Columns 8 qq .. 8 qq + 7 of a group: int8 codes bytes 8 qq .. 8 qq + 7;
+// 6-bit codes bytes 8 (qq >> 1) .. + 7 of the group's 16, low nibbles for
+// even qq, high for odd (byte j of 16-column block b holds columns j and
+// j + 8 of the block).
+__global__ void gather_sym(const uint8_t* codes, const uint32_t* hb,
+                           const int8_t* qsp, const uint16_t* dp, int bits,
+                           int n, int in, float* w, const int64_t* idx,
+                           int src_rows) {
+  const int per_row = in >> 3;
+  const long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (long)n * per_row) return;
+  const int orow = (int)(t / per_row), k = (int)(t % per_row);
+  const int g = k >> 2, qq = k & 3;
+  const int ng = in >> 5, nsb = in >> 8;
+  const int row = src_row(idx, orow, src_rows);
+  const float d = f16_bits_to_f32(dp[(size_t)row * nsb + (g >> 3)]);
+  const float sc = f16_round(
+      ((float)qsp[(size_t)row * (in >> 4) + 2 * g + (qq >> 1)] * d));
+  const size_t gi = (size_t)row * ng + g;
+  float o[8];
+  if (bits == 8) {
+    const uint2 cb = *reinterpret_cast<const uint2*>(
+        codes + (size_t)row * in + (size_t)g * 32 + 8 * qq);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t byte = ((j < 4 ? cb.x : cb.y) >> (8 * (j & 3))) & 0xFFu;
+      o[j] = (float)(int)(int8_t)byte * sc;
+    }
+  } else {
+    const int b0 = (qq >> 1) * 8, half = qq & 1;
+    const uint2 cb = *reinterpret_cast<const uint2*>(codes + gi * 16 + b0);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t v = ((j < 4 ? cb.x : cb.y) >> (8 * (j & 3))) & 0xFFu;
+      uint32_t u = half ? (v >> 4) : (v & 15u);
+      u |= high_bits_crumb(hb + gi * 2, b0 + j, half) << 4;
+      o[j] = (float)((int)u - 32) * sc;
+    }
+  }
+  float4* out = reinterpret_cast<float4*>(w + (size_t)orow * in + 8 * k);
+  out[0] = make_float4(o[0], o[1], o[2], o[3]);
+  out[1] = make_float4(o[4], o[5], o[6], o[7]);
+}
+
 __global__ void dq_rtn8(const int8_t* codes, const uint16_t* scale, int rows,
                         int in, float* w, int ld, const int64_t* idx,
                         int src_rows) {
@@ -377,10 +423,11 @@ int rwkvq_gather_rows_f32(int kind, int bits, const uint8_t* q,
   } else if (kind == 1) {     // sym: aux0 = qs, aux1 = d
     if (in % 256 || (bits != 6 && bits != 8) || (bits == 6 && !hb))
       return RWKVQ_ERR_ARG;
-    long n = (long)n_idx * (in / 32);
-    hipLaunchKernelGGL(dq_sym, grid_for(n, 256), dim3(256), 0, s, q, hb,
-                       (const int8_t*)aux0, aux1, bits, n_idx, in, out, in,
-                       idx, src_rows);
+    if (reinterpret_cast<uintptr_t>(out) & 15) return RWKVQ_ERR_ARG;
+    long n = (long)n_idx * (in / 8);
+    hipLaunchKernelGGL(gather_sym, grid_for(n, 256), dim3(256), 0, s, q, hb,
+                       (const int8_t*)aux0, aux1, bits, n_idx, in, out, idx,
+                       src_rows);
   } else if (kind == 2) {     // rtn@8: aux1 = scale
     long n = (long)n_idx * in;
     hipLaunchKernelGGL(dq_rtn8, grid_for(n, 256), dim3(256), 0, s,

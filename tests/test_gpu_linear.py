@@ -202,15 +202,22 @@ def test_shape_errors_raise():
                   _lib.stream_handle())
 
 
-@pytest.mark.parametrize("bits", [4, 5, 6])
+@pytest.mark.parametrize("kind,bits", [("sb6", 4), ("sb6", 5), ("sb6", 6),
+                                       ("sym", 6), ("sym", 8), ("rtn", 8)])
 @pytest.mark.parametrize("n_idx", [1, 8, 37])
-def test_gather_rows_sb6_bit_exact(bits, n_idx):
-    """The embedding gather (rwkvq_gather_rows_f32, sb6) == rows of the
-    oracle dequant bit for bit, indices clamped into the table."""
-    print(f"gather sb6@{bits} n_idx {n_idx}", flush=True)
+def test_gather_rows_bit_exact(kind, bits, n_idx):
+    """The embedding gather (rwkvq_gather_rows_f32) == rows of the oracle
+    dequant bit for bit, indices clamped into the table."""
+    print(f"gather {kind}@{bits} n_idx {n_idx}", flush=True)
     w = _w(40, 2560, seed=17, degenerate=True, outliers=3)
-    qt = qt_for("sb6", bits, w)
-    lin = GwQuantLinear(qt)
+    qt = qt_for(kind, bits, w)
+    lin = LIN[kind](qt)
+    if kind == "sb6":
+        args = (0, bits, lin.nib, lin.hb, lin.rec, None)
+    elif kind == "sym":
+        args = (1, bits, lin.codes, lin.hb, lin.qs, lin.d)
+    else:
+        args = (2, 8, lin.codes, None, None, lin.scale)
     rng = np.random.default_rng(n_idx)
     ids = rng.integers(0, 40, size=n_idx)
     ids[0] = 39
@@ -218,8 +225,8 @@ def test_gather_rows_sb6_bit_exact(bits, n_idx):
         ids[1], ids[2] = -5, 1000          # clamped to 0 and 39
     idx = torch.from_numpy(ids.astype(np.int64)).cuda()
     out = torch.full((n_idx, 2560), float("nan"), device="cuda")
-    _lib.call("rwkvq_gather_rows_f32", 0, bits, _lib.ptr(lin.nib),
-              _lib.ptr(lin.hb), _lib.ptr(lin.rec), None, 40, 2560,
+    _lib.call("rwkvq_gather_rows_f32", args[0], args[1],
+              *[_lib.ptr(t) for t in args[2:]], 40, 2560,
               _lib.ptr(idx), n_idx, _lib.ptr(out), _lib.stream_handle())
     ref = cr.dequant_qt(qt)[np.clip(ids, 0, 39)]
     _assert_same_bits(out.cpu().numpy(), ref)
