@@ -249,6 +249,19 @@ int rwkvq_gather_rows_f32(int kind, int bits, const uint8_t* q,
                           const int64_t* idx, int n_idx, float* out,
                           void* stream);
 
+/* The row gather above fused with the LayerNorm that follows it (ln0):
+ * out[o, :] = LN(gather(o)) with weight w, bias b, eps -- bit-exact with
+ * rwkvq_gather_rows_f32 followed by rwkvq_layer_norm, in one launch (one
+ * workgroup per output row).  in <= 4096, in % 8 == 0 (kinds 0 and 1:
+ * in % 256 == 0).
+ * Replaces: emb gather + ln0 of the first block
+ *   (reference: rwkv_quant/backends/metal/quant_model.py:853-857, 975-976). */
+int rwkvq_gather_ln_f32(int kind, int bits, const uint8_t* q,
+                        const uint32_t* hb, const void* aux0,
+                        const uint16_t* aux1, int src_rows, int in,
+                        const int64_t* idx, int n_idx, const float* w,
+                        const float* b, float eps, float* out, void* stream);
+
 /* ------------------------------------------------------- RWKV-7 blocks
  * Row layer norm (two-pass mean/variance): y = (x - mean) / sqrt(var + eps)
  * * w + b over rows of D (x and y may alias).

@@ -5,6 +5,7 @@
 // contraction), exactly as the numpy reference computes them
 // (reference: rwkv_quant/formats/codec.py:183-292).
 #include "rwkvq_common.h"
+#include "gather_cols.h"
 
 // products and sums must round separately, as numpy does: forbid the
 // a*b+c -> fma contraction hipcc applies by default
@@ -13,24 +14,6 @@
 using namespace rwkvq;
 
 namespace {
-
-// code bits 4/5 of column c (0..31) of a 32-column group from the device
-// high-bit words.  `pair_of` maps the column to (pair i, half).
-__device__ __forceinline__ uint32_t high_bits_crumb(const uint32_t* hw, int i,
-                                                    int half) {
-  uint32_t H = hw[i >> 3];
-  int sh = 2 * (i & 7) + 16 * half;
-  return (H >> sh) & 3u;
-}
-
-// `idx` (optional) gathers rows: output row o is source row
-// min(idx[o], src_rows - 1) -- the embedding lookup.
-__device__ __forceinline__ int src_row(const int64_t* idx, int o,
-                                       int src_rows) {
-  if (!idx) return o;
-  long v = idx[o];
-  return (int)(v < 0 ? 0 : (v >= src_rows ? src_rows - 1 : v));
-}
 
 __global__ void dq_sb6(const uint8_t* nib, const uint32_t* hb,
                        const uint8_t* rec, int bits, int rows, int in,
@@ -70,10 +53,9 @@ __global__ void dq_sb6(const uint8_t* nib, const uint32_t* hb,
 }
 
 // Row gather of sb6 codes (the embedding lookup, a few rows): one thread
-// per 8 consecutive columns of a 32-column group -- the group's 16-byte
-// record and the thread's 8 code bytes in one load each, the 8 outputs in
-// two float4 stores (consecutive threads, consecutive columns).  Per
-// column the arithmetic of dq_sb6.
+// per 8 consecutive columns (sb6_cols8: the group's 16-byte record and the
+// thread's 8 code bytes in one load each), the 8 outputs in two float4
+// stores (consecutive threads, consecutive columns).
 __global__ void gather_sb6(const uint8_t* nib, const uint32_t* hb,
                            const uint8_t* rec, int bits, int n, int in,
                            float* w, const int64_t* idx, int src_rows) {
@@ -81,40 +63,8 @@ __global__ void gather_sb6(const uint8_t* nib, const uint32_t* hb,
   const long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= (long)n * per_row) return;
   const int orow = (int)(t / per_row), k = (int)(t % per_row);
-  const int g = k >> 2, qq = k & 3;
-  const int ng = in >> 5, nsb = in >> 8;
-  const int row = src_row(idx, orow, src_rows);
-  // record bytes 0..5: the 6-bit qs fields, 6..11: the qm fields,
-  // 12..13: d, 14..15: dm (fp16)
-  const uint4 r4 = *reinterpret_cast<const uint4*>(
-      rec + ((size_t)row * nsb + (g >> 3)) * 16);
-  const uint64_t s0 = (uint64_t)r4.x | ((uint64_t)(r4.y & 0xFFFFu) << 32);
-  const uint64_t s1 = (uint64_t)(r4.y >> 16) | ((uint64_t)r4.z << 16);
-  const int kb = g & 7;
-  const uint32_t qs = (uint32_t)(s0 >> (6 * kb)) & 63u;
-  const int qm = (int)((uint32_t)(s1 >> (6 * kb)) & 63u) - 31;
-  const float d = f16_bits_to_f32(r4.w & 0xFFFFu);
-  const float dm = f16_bits_to_f32(r4.w >> 16);
-  const float s = fmaxf(f16_round(((float)qs * d)), 1e-8f);
-  const float m = f16_round(((float)qm * dm));
-  // columns 8 qq .. 8 qq + 7: code bytes i0 .. i0 + 7, low or high nibbles
-  const int i0 = (qq & 1) * 8, half = qq >> 1;
-  const size_t gi = (size_t)row * ng + g;
-  const uint2 nb = *reinterpret_cast<const uint2*>(nib + gi * 16 + i0);
-  const uint32_t hw5 = bits == 5 ? hb[gi] : 0u;
   float o[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int i = i0 + j, c = half * 16 + i;
-    const uint32_t byte = ((j < 4 ? nb.x : nb.y) >> (8 * (j & 3))) & 0xFFu;
-    uint32_t q = half ? (byte >> 4) : (byte & 15u);
-    if (bits == 5) {
-      q |= ((hw5 >> c) & 1u) << 4;
-    } else if (bits == 6) {
-      q |= high_bits_crumb(hb + gi * 2, i, half) << 4;
-    }
-    o[j] = (float)q * s + m;
-  }
+  sb6_cols8(nib, hb, rec, bits, in, src_row(idx, orow, src_rows), k, o);
   float4* out = reinterpret_cast<float4*>(w + (size_t)orow * in + 8 * k);
   out[0] = make_float4(o[0], o[1], o[2], o[3]);
   out[1] = make_float4(o[4], o[5], o[6], o[7]);
@@ -150,12 +100,7 @@ __global__ void dq_sym(const uint8_t* codes, const uint32_t* hb,
   }
 }
 
-// Row gather of sym codes, laid out as gather_sb6 (8 consecutive columns
-// per thread, two float4 stores); per column the arithmetic of dq_sym.
-// Columns 8 qq .. 8 qq + 7 of a group: int8 codes bytes 8 qq .. 8 qq + 7;
-// 6-bit codes bytes 8 (qq >> 1) .. + 7 of the group's 16, low nibbles for
-// even qq, high for odd (byte j of 16-column block b holds columns j and
-// j + 8 of the block).
+// Row gather of sym codes, laid out as gather_sb6 (sym_cols8).
 __global__ void gather_sym(const uint8_t* codes, const uint32_t* hb,
                            const int8_t* qsp, const uint16_t* dp, int bits,
                            int n, int in, float* w, const int64_t* idx,
@@ -164,33 +109,9 @@ __global__ void gather_sym(const uint8_t* codes, const uint32_t* hb,
   const long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= (long)n * per_row) return;
   const int orow = (int)(t / per_row), k = (int)(t % per_row);
-  const int g = k >> 2, qq = k & 3;
-  const int ng = in >> 5, nsb = in >> 8;
-  const int row = src_row(idx, orow, src_rows);
-  const float d = f16_bits_to_f32(dp[(size_t)row * nsb + (g >> 3)]);
-  const float sc = f16_round(
-      ((float)qsp[(size_t)row * (in >> 4) + 2 * g + (qq >> 1)] * d));
-  const size_t gi = (size_t)row * ng + g;
   float o[8];
-  if (bits == 8) {
-    const uint2 cb = *reinterpret_cast<const uint2*>(
-        codes + (size_t)row * in + (size_t)g * 32 + 8 * qq);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const uint32_t byte = ((j < 4 ? cb.x : cb.y) >> (8 * (j & 3))) & 0xFFu;
-      o[j] = (float)(int)(int8_t)byte * sc;
-    }
-  } else {
-    const int b0 = (qq >> 1) * 8, half = qq & 1;
-    const uint2 cb = *reinterpret_cast<const uint2*>(codes + gi * 16 + b0);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const uint32_t v = ((j < 4 ? cb.x : cb.y) >> (8 * (j & 3))) & 0xFFu;
-      uint32_t u = half ? (v >> 4) : (v & 15u);
-      u |= high_bits_crumb(hb + gi * 2, b0 + j, half) << 4;
-      o[j] = (float)((int)u - 32) * sc;
-    }
-  }
+  sym_cols8(codes, hb, qsp, dp, bits, in, src_row(idx, orow, src_rows), k,
+            o);
   float4* out = reinterpret_cast<float4*>(w + (size_t)orow * in + 8 * k);
   out[0] = make_float4(o[0], o[1], o[2], o[3]);
   out[1] = make_float4(o[4], o[5], o[6], o[7]);

@@ -16,6 +16,7 @@
 //   out = ((GN(y) * ln_x_w + ln_x_b) + (sum_head r * k' * r_k) * v') * g
 //         (group norm per head, two-pass, eps 64e-5)
 #include "rwkvq_common.h"
+#include "gather_cols.h"
 
 #include <mutex>
 
@@ -84,6 +85,56 @@ layer_norm_k(const float* x, const float* __restrict__ w,
   float mean, rstd;
   row_stats(v, D, eps, sh, mean, rstd);
   float* yr = y + (size_t)blockIdx.x * D;
+#pragma unroll
+  for (int e = 0; e < kMaxE; ++e) {
+    const int c = threadIdx.x + e * kRowThreads;
+    if (c < D) yr[c] = (v[e] - mean) * rstd * cw[e] + cb[e];
+  }
+}
+
+// Embedding row gather fused with the LayerNorm after it (ln0): one
+// workgroup per output row decodes the row straight from the packed table
+// into LDS (8 consecutive columns per thread, the arithmetic of the row
+// gather), then runs layer_norm_k's LayerNorm over it with the same column
+// ownership and reduction order -- the output equals gather + layer_norm_k
+// bit for bit, one launch instead of two.
+// KIND 0 = sb6 (aux0 = rec), 1 = sym (aux0 = qs, aux1 = d), 2 = rtn@8
+// (aux1 = scale).
+template <int KIND>
+__global__ void __launch_bounds__(kRowThreads)
+gather_ln_k(const uint8_t* q, const uint32_t* hb, const void* aux0,
+            const uint16_t* aux1, int bits, int src_rows, int D,
+            const int64_t* idx, const float* __restrict__ w,
+            const float* __restrict__ b, float* y, float eps) {
+  __shared__ float sh[16];
+  __shared__ float4 s_row4[kRowThreads * kMaxE / 4];
+  float* s_row = reinterpret_cast<float*>(s_row4);
+  const int orow = blockIdx.x;
+  const int row = src_row(idx, orow, src_rows);
+  for (int k = threadIdx.x; k < D / 8; k += kRowThreads) {
+    float o[8];
+    if constexpr (KIND == 0)
+      sb6_cols8(q, hb, static_cast<const uint8_t*>(aux0), bits, D, row, k, o);
+    else if constexpr (KIND == 1)
+      sym_cols8(q, hb, static_cast<const int8_t*>(aux0), aux1, bits, D, row,
+                k, o);
+    else
+      rtn8_cols8(reinterpret_cast<const int8_t*>(q), aux1, D, row, k, o);
+    s_row4[2 * k] = make_float4(o[0], o[1], o[2], o[3]);
+    s_row4[2 * k + 1] = make_float4(o[4], o[5], o[6], o[7]);
+  }
+  float v[kMaxE], cw[kMaxE], cb[kMaxE];
+  load_row(w, D, cw);
+  load_row(b, D, cb);
+  __syncthreads();
+#pragma unroll
+  for (int e = 0; e < kMaxE; ++e) {
+    const int c = threadIdx.x + e * kRowThreads;
+    v[e] = c < D ? s_row[c] : 0.f;
+  }
+  float mean, rstd;
+  row_stats(v, D, eps, sh, mean, rstd);
+  float* yr = y + (size_t)orow * D;
 #pragma unroll
   for (int e = 0; e < kMaxE; ++e) {
     const int c = threadIdx.x + e * kRowThreads;
@@ -1262,6 +1313,40 @@ int rwkvq_layer_norm(const float* x, const float* w, const float* b, float* y,
   if (rows <= 0 || D <= 0 || D > kRowThreads * kMaxE) return RWKVQ_ERR_ARG;
   hipLaunchKernelGGL(layer_norm_k, dim3(rows), dim3(256), 0,
                      (hipStream_t)stream, x, w, b, y, D, eps);
+  return ok_launch();
+}
+
+int rwkvq_gather_ln_f32(int kind, int bits, const uint8_t* q,
+                        const uint32_t* hb, const void* aux0,
+                        const uint16_t* aux1, int src_rows, int in,
+                        const int64_t* idx, int n_idx, const float* w,
+                        const float* b, float eps, float* out,
+                        void* stream) {
+  if (n_idx <= 0 || src_rows <= 0 || in <= 0 || !idx || !w || !b || !out ||
+      in > kRowThreads * kMaxE || in % 8)
+    return RWKVQ_ERR_ARG;
+  hipStream_t s = (hipStream_t)stream;
+  if (kind == 0) {            // sb6: aux0 = rec
+    if (in % 256 || bits < 4 || bits > 6 || (bits > 4 && !hb) || !aux0)
+      return RWKVQ_ERR_ARG;
+    hipLaunchKernelGGL(gather_ln_k<0>, dim3(n_idx), dim3(kRowThreads), 0, s,
+                       q, hb, aux0, aux1, bits, src_rows, in, idx, w, b, out,
+                       eps);
+  } else if (kind == 1) {     // sym: aux0 = qs, aux1 = d
+    if (in % 256 || (bits != 6 && bits != 8) || (bits == 6 && !hb) ||
+        !aux0 || !aux1)
+      return RWKVQ_ERR_ARG;
+    hipLaunchKernelGGL(gather_ln_k<1>, dim3(n_idx), dim3(kRowThreads), 0, s,
+                       q, hb, aux0, aux1, bits, src_rows, in, idx, w, b, out,
+                       eps);
+  } else if (kind == 2) {     // rtn@8: aux1 = scale
+    if (!aux1) return RWKVQ_ERR_ARG;
+    hipLaunchKernelGGL(gather_ln_k<2>, dim3(n_idx), dim3(kRowThreads), 0, s,
+                       q, hb, aux0, aux1, 8, src_rows, in, idx, w, b, out,
+                       eps);
+  } else {
+    return RWKVQ_ERR_ARG;
+  }
   return ok_launch();
 }
 

@@ -60,6 +60,8 @@ SIGNATURES = {
     "rwkvq_dequant_f16": [_I, _P, _P, _P, _P, _P, _I, _I, _P, _I, _P],
     "rwkvq_gather_rows_f32": [_I, _I, _P, _P, _P, _P, _I, _I, _P, _I, _P,
                               _P],
+    "rwkvq_gather_ln_f32": [_I, _I, _P, _P, _P, _P, _I, _I, _P, _I, _P, _P,
+                            _F, _P, _P],
     "rwkvq_layer_norm": [_P, _P, _P, _P, _I, _I, _F, _P],
     "rwkvq_shift_lerp": [_P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _P],
     "rwkvq_shift_lerp_f16": [_P, _P, _P, _P, _P, _I, _P, _I, _P, _I, _I, _I,

@@ -153,6 +153,22 @@ class EmbTable:
                   _stream())
         return out
 
+    def gather_ln_into(self, idx, w, b, eps, out):
+        """out [n, D] = LayerNorm(emb[idx]) with (w, b, eps): one launch for
+        a packed table (bit-exact with gather_into + rwkvq_layer_norm)."""
+        if self.dense is not None:
+            self.gather_into(idx, out)
+            _lib.call("rwkvq_layer_norm", _lib.ptr(out), _lib.ptr(w),
+                      _lib.ptr(b), _lib.ptr(out), idx.numel(), self.dim, eps,
+                      _stream())
+            return out
+        q, hb, a0, a1 = self.args
+        _lib.call("rwkvq_gather_ln_f32", self.kind, self.bits, _lib.ptr(q),
+                  _lib.ptr(hb), _lib.ptr(a0), _lib.ptr(a1), self.vocab,
+                  self.dim, _lib.ptr(idx), idx.numel(), _lib.ptr(w),
+                  _lib.ptr(b), eps, _lib.ptr(out), _stream())
+        return out
+
 
 class _Work:
     """Activation buffers for N = B*T rows (reused across layers)."""
@@ -724,9 +740,8 @@ class QuantRWKV7:
         N, C, H = B * T, self.n_embd, self.n_head
         st = _stream()
         x = wk.x
-        self.emb.gather_into(idx.reshape(-1), x)
-        _lib.call("rwkvq_layer_norm", _lib.ptr(x), _lib.ptr(self.ln0_w),
-                  _lib.ptr(self.ln0_b), _lib.ptr(x), N, C, 1e-5, st)
+        self.emb.gather_ln_into(idx.reshape(-1), self.ln0_w, self.ln0_b, 1e-5,
+                                x)
         mk = self._persistent(B, T)
         if mk is not None:
             mk.run(states, out_states, wk, st)

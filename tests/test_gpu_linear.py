@@ -230,3 +230,38 @@ def test_gather_rows_bit_exact(kind, bits, n_idx):
               _lib.ptr(idx), n_idx, _lib.ptr(out), _lib.stream_handle())
     ref = cr.dequant_qt(qt)[np.clip(ids, 0, 39)]
     _assert_same_bits(out.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("kind,bits", [("sb6", 4), ("sb6", 5), ("sb6", 6),
+                                       ("sym", 6), ("sym", 8), ("rtn", 8)])
+@pytest.mark.parametrize("n_idx", [1, 37])
+def test_gather_ln_equals_gather_then_layer_norm(kind, bits, n_idx):
+    """rwkvq_gather_ln_f32 (the embedding gather fused with ln0) ==
+    rwkvq_gather_rows_f32 followed by rwkvq_layer_norm, bit for bit."""
+    print(f"gather+ln {kind}@{bits} n_idx {n_idx}", flush=True)
+    D = 2560
+    w = _w(40, D, seed=19, outliers=3)
+    qt = qt_for(kind, bits, w)
+    lin = LIN[kind](qt)
+    if kind == "sb6":
+        args = (0, bits, lin.nib, lin.hb, lin.rec, None)
+    elif kind == "sym":
+        args = (1, bits, lin.codes, lin.hb, lin.qs, lin.d)
+    else:
+        args = (2, 8, lin.codes, None, None, lin.scale)
+    g = torch.Generator().manual_seed(n_idx)
+    lw = (1 + 0.1 * torch.randn(D, generator=g)).cuda()
+    lb = (0.1 * torch.randn(D, generator=g)).cuda()
+    ids = np.random.default_rng(n_idx).integers(-2, 45, size=n_idx)
+    idx = torch.from_numpy(ids.astype(np.int64)).cuda()
+    ptrs = [_lib.ptr(t) for t in args[2:]]
+    ref = torch.empty(n_idx, D, device="cuda")
+    _lib.call("rwkvq_gather_rows_f32", args[0], args[1], *ptrs, 40, D,
+              _lib.ptr(idx), n_idx, _lib.ptr(ref), _lib.stream_handle())
+    _lib.call("rwkvq_layer_norm", _lib.ptr(ref), _lib.ptr(lw), _lib.ptr(lb),
+              _lib.ptr(ref), n_idx, D, 1e-5, _lib.stream_handle())
+    out = torch.full((n_idx, D), float("nan"), device="cuda")
+    _lib.call("rwkvq_gather_ln_f32", args[0], args[1], *ptrs, 40, D,
+              _lib.ptr(idx), n_idx, _lib.ptr(lw), _lib.ptr(lb), 1e-5,
+              _lib.ptr(out), _lib.stream_handle())
+    assert torch.equal(out, ref)
