@@ -30,6 +30,7 @@ FORMAT_PAIRS = ((F_SB6_5, F_SB6_4), (F_SYM8, F_SYM6))
 DOWN_ROWS_PER_WG = 8            # LoRA down rows per workgroup (2 per wave)
 DOWN_WGS = 64                   # workgroups left for them beside r/k/v
 MAX_TABLES = 4
+MAX_RANK = 256                  # one rank position per thread of a workgroup
 
 
 class MkMat(ctypes.Structure):
@@ -146,7 +147,9 @@ class PersistentDecode:
                 return "formats differ between layers"
             pair = f
             ranks = [tm.lora_q[b][0] for b in tm.lora_q]
-            if any(r % 16 for r in ranks) or sum(ranks) > self.max_cat:
+            # the WKV phase stages one rank position per thread (256)
+            if any(r % 16 or r > MAX_RANK for r in ranks) or \
+                    sum(ranks) > self.max_cat:
                 return "LoRA ranks"
             if sum(-(-r // DOWN_ROWS_PER_WG) for r in ranks) > DOWN_WGS:
                 return "LoRA down rows"

@@ -106,3 +106,35 @@ def test_persistent_decode_descriptor_layout():
     assert wgs.value in (256, 512)
     assert bw.value >= 2 * (wgs.value // 32) * 32 + 64
     assert mc.value >= 288        # the 1.5B shape's four LoRA ranks
+
+
+def test_persistent_decode_shape_check(monkeypatch):
+    """PersistentDecode's host check (no device): the 1.5B LoRA ranks pass;
+    a rank above 256 (the WKV phase stages one rank position per thread)
+    or more than 64 down-product workgroups is refused before anything is
+    allocated."""
+    from types import SimpleNamespace
+    from rwkv_quant.backends.hip import decode_mk as dm
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.fail(f"{_lib.LIB_PATH} not built")
+    monkeypatch.setattr(dm, "_fmt", lambda lin: lin)
+
+    def model(ranks):
+        tm = SimpleNamespace(rkv_fused=dm.F_SB6_5, o_proj=dm.F_SB6_5,
+                             lora_q={b: (r, None, None)
+                                     for b, r in zip("wavg", ranks)})
+        cm = SimpleNamespace(key=dm.F_SB6_4, value=dm.F_SB6_4)
+        return SimpleNamespace(n_embd=2048, ffn=8192, head_size=64,
+                               blocks=[SimpleNamespace(tmix=tm, cmix=cm)])
+
+    def why(ranks):
+        pd = dm.PersistentDecode.__new__(dm.PersistentDecode)
+        pd.model, pd.max_cat = model(ranks), 640
+        return pd._check()
+
+    assert why((96, 96, 64, 256)) == ""
+    assert why((64, 64, 32, 320)) == "LoRA ranks"
+    assert why((96, 96, 64, 40)) == "LoRA ranks"            # not % 16
+    assert why((256, 256, 64, 64)) == "LoRA down rows"      # 80 workgroups
+    pd = dm.PersistentDecode(model((64, 64, 32, 320)))
+    assert not pd.ok and pd.why == "LoRA ranks"
