@@ -123,3 +123,30 @@ def test_barrier_timeout_is_reported(wide):
         model.step(tok, model.init_state(1))
         torch.cuda.synchronize()
     assert not mk.error_flag()
+
+
+def test_full_depth_reduction_matches_oracle():
+    """The 1.5B-shaped REDUCTION model (24 layers, vocab 65536; projections
+    sym@8, channel mix sym@6) on the persistent kernel: three graph decode
+    steps from a zero state against the float64 oracle, logits within 1e-2
+    max-abs, the barrier error flag clear."""
+    from rwkv_quant.models.synthetic import checkpoint_to
+    print("persistent decode, full-depth REDUCTION vs oracle", flush=True)
+    ck = quantized_model("reduction", n_layer=24, n_embd=2048, vocab=65536,
+                         seed=3, device="cuda")
+    model = qm.QuantRWKV7(ck)
+    mk = model._persistent(1, 1)
+    assert mk is not None, model._mk.why
+    orc = RWKV7Oracle(checkpoint_to(ck, "cpu"))
+    del ck
+    idx = np.random.default_rng(8).integers(0, 65536, size=(1, 3))
+    st_o, st_g = orc.init_state(1), model.init_state(1)
+    for t in range(3):
+        tok = idx[:, t:t + 1]
+        ro, st_o = orc.forward_stateful(tok, st_o)
+        lg, st_g = model.step(torch.from_numpy(tok), st_g)
+        err = _maxabs(lg.cpu().numpy(), ro)
+        print(f"step {t}: {err:.2e} (logit scale {np.abs(ro).max():.2f})",
+              flush=True)
+        assert err < 1e-2, t
+    assert not mk.error_flag()
