@@ -138,3 +138,29 @@ def test_persistent_decode_shape_check(monkeypatch):
     assert why((256, 256, 64, 64)) == "LoRA down rows"      # 80 workgroups
     pd = dm.PersistentDecode(model((64, 64, 32, 320)))
     assert not pd.ok and pd.why == "LoRA ranks"
+
+
+def test_gather_ln_rejects_bad_arguments():
+    """rwkvq_gather_ln_f32's host-side checks (no device call): widths the
+    row kernel cannot hold, widths off the format's blocks, a missing index
+    or LayerNorm vector, an unknown kind -> RWKVQ_ERR_ARG."""
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.fail(f"{_lib.LIB_PATH} not built")
+    f = _lib.load().rwkvq_gather_ln_f32
+    P = ctypes.c_void_p
+    dummy = P(256)                         # never dereferenced: checks first
+
+    def call(kind, bits, src_rows, width, idx, n, w, b, aux1=dummy):
+        return f(kind, bits, dummy, dummy, dummy, aux1, src_rows, width, idx,
+                 n, w, b, ctypes.c_float(1e-5), dummy, None)
+
+    ERR = 1001
+    assert call(0, 5, 8, 4352, dummy, 1, dummy, dummy) == ERR   # > 4096
+    assert call(0, 5, 8, 2050, dummy, 1, dummy, dummy) == ERR   # % 8
+    assert call(0, 5, 8, 2056, dummy, 1, dummy, dummy) == ERR   # % 256
+    assert call(1, 7, 8, 2048, dummy, 1, dummy, dummy) == ERR   # sym bits
+    assert call(0, 5, 8, 2048, None, 1, dummy, dummy) == ERR    # no idx
+    assert call(0, 5, 8, 2048, dummy, 0, dummy, dummy) == ERR   # no rows
+    assert call(0, 5, 8, 2048, dummy, 1, None, dummy) == ERR    # no weight
+    assert call(2, 8, 8, 2048, dummy, 1, dummy, dummy, None) == ERR
+    assert call(3, 8, 8, 2048, dummy, 1, dummy, dummy) == ERR   # kind
